@@ -1,0 +1,276 @@
+"""Benchmark: fused cold-page egress + ingress of a 1 GiB BF16 KV prefix on one MI355X.
+
+A step is one egress pass (quantize -> ChaCha20 -> SipHash-2-4-128) and one
+ingress pass (verify -> decrypt -> dequantize) over the whole prefix, with
+pages resident in HBM and outputs preallocated: 4096 tokens x 64 layers =
+16384 pages of 16 tokens x 8 KV heads x head_dim 128, K and V in BF16
+(1 GiB hot), encoded through the descriptor API in one launch per direction.
+
+  value     = 2 x hot bytes x steps / (egress + ingress time)   [GB/s]
+  roofline  = the egress kernel's algorithmic bytes (hot read + wire written)
+              per launch / its average launch time (HIP events on its stream),
+              against MI355X's 8 TB/s HBM peak
+  cpu_baseline = the reference's own C++ codec (oracle/_ref, compiled from the
+              reference sources) on this host's cores, FP16 (its only dtype),
+              on a bounded sample of the same pages
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+METRIC = "hot-byte GB/s egress+ingress, 1 GiB BF16 prefix, 1 GPU; % of HBM roofline"
+HBM_PEAK_GBPS = 8000.0
+
+
+def _package():
+    name = "vlx_tee_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    root = REPO / "vlx-tee_amd"
+    spec = importlib.util.spec_from_file_location(name, root / "__init__.py",
+                                                  submodule_search_locations=[str(root)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def run_gpu(wname: str, steps: int, warmup: int) -> dict:
+    import numpy as np
+    import torch
+
+    _package().load_native()
+    import vlx_tee_amd.pages as P
+    from vlx_tee_amd.workloads import MODEL_HASH, TENANT_HASH, WORKLOADS, generate, page_metadata, session_keys
+
+    w = WORKLOADS[wname]
+    dev = torch.device("cuda:0")
+    keys = session_keys()
+    _log(f"{wname}: generating {w.n_pages} pages on {dev}")
+    k, v = generate(w, dev, torch.bfloat16)
+    th, seq, layers = page_metadata(w)
+    blobs = torch.empty((w.n_pages, w.blob_bytes), dtype=torch.uint8, device=dev)
+    ko = torch.empty_like(k)
+    vo = None if v is None else torch.empty_like(v)
+    status = torch.full((w.n_pages,), -1, dtype=torch.int32, device=dev)
+    d_out = P.build_descriptors(k, v, blobs, th, seq, layers)
+    d_in = P.build_descriptors(ko, vo, blobs, th, seq, layers)
+    geo = dict(num_tokens=w.num_tokens, num_heads=w.num_heads, head_dim=w.head_dim,
+               rope_dim=w.rope_dim, dtype=torch.bfloat16, is_mla_single_buffer=w.mla)
+
+    def egress():
+        P.egress(d_out, w.n_pages, preset=w.preset, rope_mode=w.rope_mode,
+                 expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
+                 model_id_hash=MODEL_HASH, **geo, **keys)
+
+    def ingress():
+        P.ingress(d_in, w.n_pages, w.blob_bytes, expected_tenant_hash=TENANT_HASH,
+                  expected_model_hash=MODEL_HASH, page_status=status, asynchronous=True, **geo, **keys)
+
+    for _ in range(warmup):
+        egress()
+        ingress()
+    torch.cuda.synchronize()
+    st = status.cpu().numpy()
+    if not (st == 0).all():
+        raise SystemExit(f"bench: {int((st != 0).sum())} pages failed verification after warmup")
+    # self-consistency: a second encode reproduces the blobs bit for bit
+    ref_blobs = blobs.clone()
+    egress()
+    torch.cuda.synchronize()
+    if not torch.equal(ref_blobs, blobs):
+        raise SystemExit("bench: egress is not deterministic")
+    del ref_blobs
+    import vlx_tee_amd.native_hip_codec as H
+
+    diag = H.device_diag()
+
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1, e2 in ev:
+        e0.record(stream)
+        egress()
+        e1.record(stream)
+        ingress()
+        e2.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    te = [a.elapsed_time(b) for a, b, _ in ev]
+    ti = [b.elapsed_time(c) for _, b, c in ev]
+    st = status.cpu().numpy()
+    if not (st == 0).all():
+        raise SystemExit("bench: pages failed verification in the timed region")
+    hot = w.n_pages * w.hot_bytes_per_page
+    wire = w.n_pages * w.blob_bytes
+    me, mi = statistics.mean(te), statistics.mean(ti)
+    res = dict(
+        workload=wname, pages=w.n_pages, hot_bytes=hot, wire_bytes=wire,
+        egress_ms=me, ingress_ms=mi, egress_ms_median=statistics.median(te),
+        ingress_ms_median=statistics.median(ti), wall_s=wall,
+        egress_hot_gbps=hot / me / 1e6, egress_wire_gbps=wire / me / 1e6,
+        ingress_hot_gbps=hot / mi / 1e6, ingress_wire_gbps=wire / mi / 1e6,
+        roundtrip_hot_gbps=2 * hot / (me + mi) / 1e6,
+        egress_hbm_frac=(hot + wire) / me / 1e6 / HBM_PEAK_GBPS,
+        ingress_hbm_frac=(hot + wire) / mi / 1e6 / HBM_PEAK_GBPS,
+        device_diag=diag,
+    )
+    del k, v, blobs, ko, vo
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(wname: str, budget_s: float) -> dict | None:
+    """The reference's C++ codec on this host (FP16), on a bounded page sample."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, str(REPO))
+    from oracle import oracle as O
+    from vlx_tee_amd.workloads import MODEL_HASH, TENANT_HASH, WORKLOADS, generate, session_keys
+
+    w = WORKLOADS[wname]
+    keys = session_keys()
+    ref = O.ref_module()
+    threads = os.cpu_count() or 1
+
+    def run(n):
+        k, v = generate(w, "cpu", torch.float16, n_pages=n)
+        th = torch.arange(n, dtype=torch.int64)
+        if ref is not None:
+            t0 = time.perf_counter()
+            blobs = ref.fused_encode_cold_pages_batch_cpu(
+                k, v, th, w.preset, w.rope_mode, w.rope_dim, w.payload_bytes, TENANT_HASH,
+                MODEL_HASH, 0, 0, 0, keys["k0"], keys["k1"], keys["mk0"], keys["mk1"],
+                keys["k2"], keys["k3"])
+            t1 = time.perf_counter()
+            ref.fused_decode_cold_pages_batch_cpu(
+                blobs, th, w.num_tokens, w.num_heads, w.head_dim, w.rope_dim, w.mla, TENANT_HASH,
+                MODEL_HASH, 0, keys["k0"], keys["k1"], keys["mk0"], keys["mk1"], keys["k2"], keys["k3"])
+            t2 = time.perf_counter()
+        else:
+            kb = k.view(torch.int16).numpy().view(np.uint16)
+            vb = None if v is None else v.view(torch.int16).numpy().view(np.uint16)
+            t0 = time.perf_counter()
+            blobs = O.egress_batch(kb, vb, th.numpy(), dtype=O.FP16, preset=w.preset,
+                                   rope_mode=w.rope_mode, rope_dim=w.rope_dim,
+                                   tenant_id_hash=TENANT_HASH, model_id_hash=MODEL_HASH, layer_id=0,
+                                   head_group_id=0, base_sequence_nonce=0, threads=threads, **keys)
+            t1 = time.perf_counter()
+            O.ingress_batch(blobs, th.numpy(), num_tokens=w.num_tokens, num_heads=w.num_heads,
+                            head_dim=w.head_dim, rope_dim=w.rope_dim, is_mla_single_buffer=w.mla,
+                            dtype=O.FP16, expected_tenant_hash=TENANT_HASH,
+                            expected_model_hash=MODEL_HASH, expected_layer_id=0, threads=1, **keys)
+            t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    te, ti = run(64)
+    per_page = (te + ti) / 64
+    n = int(max(64, min(w.n_pages, budget_s / max(per_page, 1e-9))))
+    te, ti = run(n)
+    hot = n * w.hot_bytes_per_page
+    egress_threads = min(n, threads)
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:  # noqa: BLE001
+        model = "unknown"
+    return dict(
+        value=2 * hot / (te + ti) / 1e9, unit="GB/s", cores=egress_threads,
+        kind="reference" if ref is not None else "port",
+        sample=(f"{n} pages of {wname} (FP16: the reference's only hot dtype), egress through "
+                f"fused_encode_cold_pages_batch_cpu on {egress_threads} std::threads, ingress through "
+                f"fused_decode_cold_pages_batch_cpu (serial on Linux, cpp:2215-2229); host "
+                f"{threads} logical CPUs, {model}"),
+        egress_hot_gbps=hot / te / 1e9, ingress_hot_gbps=hot / ti / 1e9,
+        egress_s=te, ingress_s=ti,
+    )
+
+
+def _traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    f = REPO / "profiles" / "hbm_traffic.json"
+    if not f.is_file():
+        return None
+    try:
+        return json.loads(f.read_text()).get(f"{kernel}/{workload}", {}).get("bytes_per_launch")
+    except Exception:  # noqa: BLE001
+        return None
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c2_k8v4_prefix1g")
+    ap.add_argument("--also", default="c2_int4_prefix1g", help="comma list of extra workloads")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the cold-page codec has no cross-GPU step "
+              "(pages shard independently); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    main_res = run_gpu(a.workload, a.steps, a.warmup)
+    extras = {}
+    for wn in [x for x in a.also.split(",") if x and x != a.workload]:
+        extras[wn] = run_gpu(wn, max(3, a.steps // 2), 2)
+    cpu = None if a.no_cpu else cpu_baseline(a.workload, a.cpu_seconds)
+
+    r = main_res
+    achieved = (r["hot_bytes"] + r["wire_bytes"]) / r["egress_ms"] / 1e6
+    out = {
+        "metric": METRIC,
+        "value": round(r["roundtrip_hot_gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(r["egress_ms"] + r["ingress_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{a.workload}: 4096 tok x 64 layers = {r['pages']} pages of 16 tok x 8 KV "
+                         "heads x head_dim 128, K+V BF16 (1 GiB hot), K8V4_ASYM + PRESERVE_FP8, "
+                         "N(0,1) with RoPE dims x8, one descriptor-batch launch per direction"),
+            "pages": r["pages"], "hot_bytes": r["hot_bytes"], "wire_bytes": r["wire_bytes"],
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "egress_fused_kernel",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic("egress_fused_kernel", a.workload),
+        },
+        "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)
+                                                  for k, v in cpu.items()},
+        "egress": {k: round(r[k], 4) for k in ("egress_ms", "egress_hot_gbps", "egress_wire_gbps", "egress_hbm_frac")},
+        "ingress": {k: round(r[k], 4) for k in ("ingress_ms", "ingress_hot_gbps", "ingress_wire_gbps", "ingress_hbm_frac")},
+        "extra_workloads": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
+                            for n, x in extras.items()},
+        "device_diag": r["device_diag"],
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,181 @@
+/*
+ * ztcp.h -- C ABI of the MI355X (gfx950) ZTCP fused cold-page codec.
+ *
+ * Egress:  quantize -> ChaCha20 (RFC 8439) -> SipHash-2-4-128 Encrypt-then-MAC.
+ * Ingress: verify tag and AAD -> decrypt -> dequantize, rejecting tampered pages.
+ *
+ * Every entry point below replaces one function of the reference's native
+ * module `ztcp_fused_cold_page_cpp` (research/baseline_codec/csrc/
+ * fused_cold_page_cpu.cpp, "cpp" below), as bound by its Python wrapper
+ * research/baseline_codec/native_fused_codec.py ("nfc").  Arguments keep the
+ * reference's names, meaning and order; torch tensors become plain device
+ * pointers plus the sizes the tensors carried.
+ *
+ * Conventions
+ *  - Page data, blobs, token hashes and status arrays are DEVICE pointers.
+ *  - Hot pages are [batch, num_tokens, num_heads, head_dim] elements of
+ *    `hot_dtype` (FP16 = the reference's only dtype, cpp:1499; BF16 = extension:
+ *    the byte layout is unchanged, scales stay fp16 on the wire).
+ *  - A blob is 32-byte header || payload || 16-byte tag (spec:17-51).
+ *  - Calls are enqueued on `stream` (a hipStream_t; NULL = the default stream).
+ *    Egress returns once enqueued.  Ingress without ZTCP_ASYNC synchronizes
+ *    the stream and returns the reference's verdict; with ZTCP_ASYNC it
+ *    returns after enqueueing and the verdict is read from `page_status`.
+ *  - Keys are passed by value and never retained (nfc:173-174 unpacks them
+ *    into the same little-endian u64 words).
+ *  - Errors are return codes, never exceptions: negative = argument / runtime
+ *    error (the TORCH_CHECK list of cpp:1925-1957, cpp:2267-2296);
+ *    positive = integrity verdict of the lowest failing page (cpp:2231-2245).
+ */
+#ifndef ZTCP_H
+#define ZTCP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Wire constants: spec:47-51, cpp:55-58. */
+#define ZTCP_MAGIC 0x5A54u
+#define ZTCP_VERSION 1u
+#define ZTCP_HEADER_BYTES 32u
+#define ZTCP_TAG_BYTES 16u
+
+/* QuantPreset (spec:54-59) and RoPEMode (spec:62-67). */
+enum { ZTCP_INT4_SYM = 1, ZTCP_K8V4_ASYM = 2, ZTCP_FP8_ONLY = 3 };
+enum { ZTCP_QUANTIZE_ALL = 0, ZTCP_PRESERVE_FP8 = 1, ZTCP_PRESERVE_RAW = 2 };
+enum { ZTCP_HOT_FP16 = 0, ZTCP_HOT_BF16 = 1 };
+
+/* Integrity verdicts: the reference's per-page status codes (cpp:2056-2057). */
+#define ZTCP_OK 0
+#define ZTCP_ERR_HEADER 1  /* KV_INTEGRITY_ERROR: magic, version, flags or size */
+#define ZTCP_ERR_AAD 2     /* CROSS_TENANT_CONTAMINATION: tenant/model/layer/token */
+#define ZTCP_ERR_MAC 3     /* KV_INTEGRITY_ERROR: MAC verification failed */
+/* Argument / runtime errors. */
+#define ZTCP_EINVAL (-1)   /* a TORCH_CHECK of the reference would fail */
+#define ZTCP_EOVERLAP (-2) /* an output aliases an input (cpp:1428-1437) */
+#define ZTCP_EHIP (-3)     /* the HIP runtime reported an error */
+#define ZTCP_EDEVICE (-4)  /* a kernel's bounded wait expired (see ztcp_device_diag) */
+
+/* Ingress flags. */
+#define ZTCP_ASYNC 0x1u          /* enqueue only; verdicts land in page_status */
+#define ZTCP_PER_PAGE 0x2u       /* extension: keep verified pages, zero failing ones;
+                                    default is the reference's all-or-nothing */
+
+typedef struct ztcp_geometry {
+    int64_t num_tokens;   /* tokens per page */
+    int64_t num_heads;    /* KV heads per page */
+    int64_t head_dim;     /* >= 16, multiple of 16 */
+    int64_t rope_dim;     /* leading RoPE columns of K, multiple of 16 */
+    int32_t hot_dtype;    /* ZTCP_HOT_FP16 / ZTCP_HOT_BF16 */
+    int32_t is_mla_single_buffer; /* 1: K only (no V buffer) */
+} ztcp_geometry;
+
+/* Per-batch AAD fields of the header (cpp:61-75). */
+typedef struct ztcp_aad {
+    uint32_t tenant_id_hash;
+    uint32_t model_id_hash;
+    uint16_t layer_id;
+    uint16_t head_group_id;
+} ztcp_aad;
+
+/* Session keys as the reference passes them: encryption key k0..k3 (LE u64
+ * words of the 32-byte key, cpp:85-100), MAC key mk0, mk1 (nfc:173-174). */
+typedef struct ztcp_keys {
+    uint64_t k0, k1, k2, k3;
+    uint64_t mk0, mk1;
+} ztcp_keys;
+
+/* One page of a paged (non-contiguous) KV pool, possibly spanning layers.
+ * Egress reads k/v and writes blob; ingress reads blob and writes k/v.  v is
+ * NULL for MLA single-buffer pages.  k, v and blob must be 16-byte aligned.
+ * The per-page fields replace the batch-wide ones of the contiguous form:
+ *   egress:  token_hash, sequence_nonce, layer_id, head_group_id go into the
+ *            page's header and nonce (cpp:1129-1140, cpp:102-110);
+ *   ingress: token_hash and layer_id are the page's expected AAD values
+ *            (cpp:2317-2323); sequence_nonce / head_group_id are not compared,
+ *            as in the reference. */
+typedef struct ztcp_page_desc {
+    void* k;
+    void* v;
+    uint8_t* blob;
+    int64_t token_hash;
+    uint64_t sequence_nonce;
+    uint16_t layer_id;
+    uint16_t head_group_id;
+    uint32_t reserved;
+} ztcp_page_desc;
+
+/* Payload bytes padded to 4 (spec:203-246, what nfc passes as
+ * expected_payload_bytes); (size_t)-1 for invalid preset / rope_mode. */
+size_t ztcp_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
+/* Unpadded minimum payload for header flags: required_payload_bytes_for_flags
+ * (cpp:1439-1474); (size_t)-1 for invalid flags. */
+size_t ztcp_required_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
+/* 32 + ztcp_payload_bytes + 16 (spec:248-250 cold_blob_bytes). */
+size_t ztcp_blob_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
+
+/* Batch egress into a preallocated [batch, 32 + expected_payload_bytes + 16]
+ * buffer.  Replaces fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004):
+ * page b is read at b * T*H*D elements, encoded with token_hashes[b] and
+ * sequence_nonce = base_sequence_nonce + b, and written at b * blob_bytes. */
+int ztcp_egress_peak_into(const void* k_pages, const void* v_pages,
+                          const int64_t* page_token_hashes, uint8_t* out_blobs,
+                          int64_t batch, const ztcp_geometry* g, int64_t preset,
+                          int64_t rope_mode, int64_t expected_payload_bytes,
+                          const ztcp_aad* aad, uint64_t base_sequence_nonce,
+                          const ztcp_keys* keys, void* stream);
+
+/* Descriptor form of the same egress for paged, multi-layer KV pools:
+ * `pages` is a DEVICE array of n_pages descriptors; tenant and model hashes
+ * come from `tenant_id_hash` / `model_id_hash`, every other header field from
+ * the page's descriptor.  Same encoding as ztcp_egress_peak_into. */
+int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages,
+                      const ztcp_geometry* g, int64_t preset, int64_t rope_mode,
+                      int64_t expected_payload_bytes, uint32_t tenant_id_hash,
+                      uint32_t model_id_hash, const ztcp_keys* keys, void* stream);
+
+/* Batch ingress into preallocated outputs.  Replaces
+ * fused_decode_cold_pages_peak_into_cpu (cpp:2250-2496): every page is
+ * checked in the reference's order (magic/version -> 1, tenant/model/layer/
+ * token hash -> 2, SipHash tag -> 3, flags/size -> 1), decrypted and
+ * dequantized according to its own header flags.  Default (all-or-nothing):
+ * if any page fails, both outputs are zeroed and the verdict of the lowest
+ * failing page is returned.  page_status (DEVICE int32[batch], may be NULL)
+ * receives every page's verdict. */
+int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
+                           const int64_t* expected_token_hashes, void* out_k_pages,
+                           void* out_v_pages, int64_t batch, const ztcp_geometry* g,
+                           uint32_t expected_tenant_hash, uint32_t expected_model_hash,
+                           uint16_t expected_layer_id, const ztcp_keys* keys,
+                           int32_t* page_status, uint32_t flags, void* stream);
+
+/* Descriptor form of the same ingress (blob in, k/v out; the expected token
+ * hash and layer id of each page come from its descriptor). */
+int ztcp_ingress_batch(const ztcp_page_desc* pages, int64_t n_pages, int64_t blob_bytes,
+                       const ztcp_geometry* g, uint32_t expected_tenant_hash,
+                       uint32_t expected_model_hash, const ztcp_keys* keys,
+                       int32_t* page_status, uint32_t flags, void* stream);
+
+/* Known-answer hooks.  ztcp_chacha20_xor replaces chacha20_rfc8439_xor_cpu
+ * (cpp:2499-2524): dst = src ^ ChaCha20(key, nonce, counter..).
+ * ztcp_siphash128 replaces siphash24_128_cpu (cpp:2526-2538).  key, nonce
+ * are HOST byte arrays; data and outputs are DEVICE pointers. */
+int ztcp_chacha20_xor(const uint8_t* src, uint8_t* dst, size_t len, const uint8_t key[32],
+                      uint32_t initial_counter, const uint8_t nonce[12], void* stream);
+int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
+                    uint8_t* tag16, void* stream);
+
+/* Device-side diagnostics of the current device: returns and clears the
+ * sticky flags a kernel's bounded waits set (0 = none). Synchronizes. */
+int ztcp_device_diag(void);
+
+/* Short description of a return code. */
+const char* ztcp_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZTCP_H */

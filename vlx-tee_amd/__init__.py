@@ -1,0 +1,19 @@
+"""MI355X-native ZTCP fused cold-page codec (gfx950 HIP kernels behind a C ABI).
+
+Modules:
+  native_hip_codec  drop-in for the reference's native module functions
+                    (research/baseline_codec/csrc/fused_cold_page_cpu.cpp:2540-2683)
+  pages             descriptor-based batch API for paged, multi-layer KV pools
+  spec              wire constants and payload sizing (cold_page_spec.py mirror)
+  workloads         synthetic page generators for the benchmark configurations
+"""
+from . import spec  # noqa: F401
+
+__all__ = ["spec", "native_hip_codec", "pages", "workloads", "load_native"]
+
+
+def load_native():
+    """Load the C-ABI library; raises if it has not been built."""
+    from . import _native
+
+    return _native.lib()

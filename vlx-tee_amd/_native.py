@@ -1,0 +1,104 @@
+"""ctypes binding of the HIP C-ABI library (include/ztcp.h -> libztcp_hip.so).
+
+The library is loaded after ``torch`` so both share torch's HIP runtime (the
+library's DT_NEEDED ``libamdhip64.so.7`` resolves to the copy torch already
+mapped).  There is no fallback: a missing library raises at load time.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+LIB_PATH = Path(__file__).resolve().parent / "libztcp_hip.so"
+
+# Return codes (include/ztcp.h).
+OK, ERR_HEADER, ERR_AAD, ERR_MAC = 0, 1, 2, 3
+EINVAL, EOVERLAP, EHIP, EDEVICE = -1, -2, -3, -4
+ASYNC, PER_PAGE = 0x1, 0x2
+HOT_FP16, HOT_BF16 = 0, 1
+
+# Every symbol include/ztcp.h declares.
+EXPORTS = (
+    "ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes",
+    "ztcp_egress_peak_into", "ztcp_egress_batch",
+    "ztcp_ingress_peak_into", "ztcp_ingress_batch",
+    "ztcp_chacha20_xor", "ztcp_siphash128",
+    "ztcp_device_diag", "ztcp_strerror",
+)
+
+
+class Geometry(C.Structure):
+    _fields_ = [("num_tokens", C.c_int64), ("num_heads", C.c_int64), ("head_dim", C.c_int64),
+                ("rope_dim", C.c_int64), ("hot_dtype", C.c_int32),
+                ("is_mla_single_buffer", C.c_int32)]
+
+
+class Aad(C.Structure):
+    _fields_ = [("tenant_id_hash", C.c_uint32), ("model_id_hash", C.c_uint32),
+                ("layer_id", C.c_uint16), ("head_group_id", C.c_uint16)]
+
+
+class Keys(C.Structure):
+    _fields_ = [("k0", C.c_uint64), ("k1", C.c_uint64), ("k2", C.c_uint64), ("k3", C.c_uint64),
+                ("mk0", C.c_uint64), ("mk1", C.c_uint64)]
+
+
+class PageDesc(C.Structure):
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("blob", C.c_void_p),
+                ("token_hash", C.c_int64), ("sequence_nonce", C.c_uint64),
+                ("layer_id", C.c_uint16), ("head_group_id", C.c_uint16),
+                ("reserved", C.c_uint32)]
+
+
+_lib: C.CDLL | None = None
+
+
+def lib() -> C.CDLL:
+    """The loaded C-ABI library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.is_file():
+        raise RuntimeError(
+            f"HIP codec library missing: {LIB_PATH} (build it with python vlx-tee_amd/build.py)")
+    L = C.CDLL(str(LIB_PATH))
+    P, G, A, K = C.c_void_p, C.POINTER(Geometry), C.POINTER(Aad), C.POINTER(Keys)
+    i64, u64, u32, u16, i32 = C.c_int64, C.c_uint64, C.c_uint32, C.c_uint16, C.c_int
+    for name in ("ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes"):
+        f = getattr(L, name)
+        f.argtypes = [G, i64, i64]
+        f.restype = C.c_size_t
+    L.ztcp_egress_peak_into.argtypes = [P, P, P, P, i64, G, i64, i64, i64, A, u64, K, P]
+    L.ztcp_egress_peak_into.restype = i32
+    L.ztcp_egress_batch.argtypes = [P, i64, G, i64, i64, i64, u32, u32, K, P]
+    L.ztcp_egress_batch.restype = i32
+    L.ztcp_ingress_peak_into.argtypes = [P, i64, P, P, P, i64, G, u32, u32, u16, K, P, u32, P]
+    L.ztcp_ingress_peak_into.restype = i32
+    L.ztcp_ingress_batch.argtypes = [P, i64, i64, G, u32, u32, K, P, u32, P]
+    L.ztcp_ingress_batch.restype = i32
+    L.ztcp_chacha20_xor.argtypes = [P, P, C.c_size_t, P, u32, P, P]
+    L.ztcp_chacha20_xor.restype = i32
+    L.ztcp_siphash128.argtypes = [P, C.c_size_t, u64, u64, P, P]
+    L.ztcp_siphash128.restype = i32
+    L.ztcp_device_diag.argtypes = []
+    L.ztcp_device_diag.restype = i32
+    L.ztcp_strerror.argtypes = [i32]
+    L.ztcp_strerror.restype = C.c_char_p
+    _lib = L
+    return L
+
+
+def strerror(code: int) -> str:
+    return lib().ztcp_strerror(code).decode()
+
+
+def geometry(num_tokens: int, num_heads: int, head_dim: int, rope_dim: int, hot_dtype: int,
+             is_mla_single_buffer: bool) -> Geometry:
+    return Geometry(num_tokens, num_heads, head_dim, rope_dim, hot_dtype, int(is_mla_single_buffer))
+
+
+def keys(k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0) -> Keys:
+    m = (1 << 64) - 1
+    return Keys(k0 & m, k1 & m, k2 & m, k3 & m, mk0 & m, mk1 & m)

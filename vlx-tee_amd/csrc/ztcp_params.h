@@ -1,0 +1,148 @@
+// ztcp_params.h -- kernel argument blocks and launch helpers shared by the
+// egress, ingress and generic translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ztcp.h"
+#include "ztcp_device.h"
+#include "ztcp_layout.h"
+
+namespace ztcp {
+
+// Sticky device diagnostics (bit flags, or-ed by kernels).
+constexpr uint32_t kDiagEgressWait = 1u;   // MAC wave's bounded wait expired
+
+// Per-device library state (allocated once per device by the host side).
+struct DeviceState {
+    uint32_t diag;             // sticky diagnostic flags
+    uint32_t pad;
+    unsigned long long fail;   // (page_index << 8) | status of the lowest failing page
+};
+
+struct EgressParams {
+    const uint8_t* k;              // contiguous K pages (hot elements, 2 bytes each)
+    const uint8_t* v;              // contiguous V pages or nullptr
+    const int64_t* token_hashes;   // [batch]
+    uint8_t* blobs;                // [batch, blob_bytes]
+    const ztcp_page_desc* descs;   // descriptor mode when non-null
+    int64_t batch;
+    int64_t page_bytes;            // T*H*D*2
+    int32_t vecs, head_dim;
+    uint32_t payload;              // expected_payload_bytes
+    uint32_t blob_bytes;
+    Layout lay;
+    ChaKey key;
+    uint64_t mk0, mk1;
+    uint64_t hdr0;                 // header bytes 0..7 (magic, version, flags, tenant)
+    uint64_t hdr1;                 // header bytes 8..15 (model, layer, head group);
+                                   // descriptor mode: only the model hash is used
+    uint32_t nonce2;               // (layer_id << 16) | head_group_id
+    uint64_t base_seq;
+    int32_t ppw;                   // pages per workgroup
+    int32_t n_batches;             // ceil(ppw * n_units / 64)
+    DeviceState* state;
+};
+
+struct IngressParams {
+    const uint8_t* blobs;          // [batch, blob_bytes]
+    const int64_t* token_hashes;   // expected token hashes [batch]
+    uint8_t* out_k;
+    uint8_t* out_v;                // nullptr for MLA single buffer
+    const ztcp_page_desc* descs;
+    int32_t* page_status;          // may be null
+    int64_t batch;
+    int64_t page_bytes;
+    int32_t vecs, head_dim;
+    uint32_t blob_bytes;
+    uint32_t payload;              // blob_bytes - 48
+    Layout lay[9];                 // layout for preset 1..3 x rope_mode 0..2
+    int32_t lay_ok[9];             // flags valid and payload >= required
+    int32_t n_units;               // the same for every valid flag combination
+    ChaKey key;
+    uint64_t mk0, mk1;
+    uint32_t exp_tenant, exp_model;
+    uint32_t exp_layer;
+    int32_t per_page;              // zero failing pages in-kernel
+    int32_t ppw;
+    int32_t n_batches;
+    DeviceState* state;
+};
+
+// Page addressing (contiguous batch or descriptor array).
+struct EgressPage {
+    const uint8_t* k;
+    const uint8_t* v;
+    uint8_t* blob;
+    uint64_t token;
+    uint64_t seq;
+    uint64_t hdr1;    // header bytes 8..15: model, layer, head group
+    uint32_t nonce2;  // (layer_id << 16) | head_group_id
+};
+
+__device__ __forceinline__ EgressPage egress_page(const EgressParams& p, int64_t page) {
+    EgressPage e;
+    if (p.descs) {
+        const ztcp_page_desc& d = p.descs[page];
+        e.k = (const uint8_t*)d.k;
+        e.v = (const uint8_t*)d.v;
+        e.blob = d.blob;
+        e.token = (uint64_t)d.token_hash;
+        e.seq = d.sequence_nonce;
+        e.hdr1 = (p.hdr1 & 0xFFFFFFFFull) | ((uint64_t)d.layer_id << 32) | ((uint64_t)d.head_group_id << 48);
+        e.nonce2 = ((uint32_t)d.layer_id << 16) | (uint32_t)d.head_group_id;
+    } else {
+        e.k = p.k + page * p.page_bytes;
+        e.v = p.v ? p.v + page * p.page_bytes : nullptr;
+        e.blob = p.blobs + page * (int64_t)p.blob_bytes;
+        e.token = (uint64_t)p.token_hashes[page];
+        e.seq = p.base_seq + (uint64_t)page;  // cpp:1979
+        e.hdr1 = p.hdr1;
+        e.nonce2 = p.nonce2;
+    }
+    return e;
+}
+
+__device__ __forceinline__ const uint8_t* ingress_blob(const IngressParams& p, int64_t page) {
+    return p.descs ? (const uint8_t*)p.descs[page].blob : p.blobs + page * (int64_t)p.blob_bytes;
+}
+__device__ __forceinline__ uint8_t* ingress_k(const IngressParams& p, int64_t page) {
+    return p.descs ? (uint8_t*)p.descs[page].k : p.out_k + page * p.page_bytes;
+}
+// nullptr when the page has no V buffer (MLA single buffer).
+__device__ __forceinline__ uint8_t* ingress_v(const IngressParams& p, int64_t page) {
+    if (p.descs) return (uint8_t*)p.descs[page].v;
+    return p.out_v ? p.out_v + page * p.page_bytes : nullptr;
+}
+__device__ __forceinline__ uint64_t ingress_token(const IngressParams& p, int64_t page) {
+    return (uint64_t)(p.descs ? p.descs[page].token_hash : p.token_hashes[page]);
+}
+__device__ __forceinline__ uint32_t ingress_layer(const IngressParams& p, int64_t page) {
+    return p.descs ? (uint32_t)p.descs[page].layer_id : p.exp_layer;
+}
+
+// Field of section `si` (0..2) selected without dynamic indexing.
+#define ZTCP_SEC_FIELD(lay, si, f) \
+    ((si) == 0 ? (lay).sec[0].f : ((si) == 1 ? (lay).sec[1].f : (lay).sec[2].f))
+
+__device__ __forceinline__ int section_of_unit(const Layout& lay, int u) {
+    return (lay.n_sec > 1 && u >= lay.sec[1].unit_begin)
+               ? ((lay.n_sec > 2 && u >= lay.sec[2].unit_begin) ? 2 : 1)
+               : 0;
+}
+
+// Host-side launchers (defined in the .hip translation units).
+hipError_t launch_egress_fused(const EgressParams& p, int dtype, int waves, hipStream_t s);
+hipError_t launch_ingress_fused(const IngressParams& p, int dtype, int waves, hipStream_t s);
+hipError_t launch_egress_generic(const EgressParams& p, int dtype, hipStream_t s);
+hipError_t launch_ingress_generic_impl(const IngressParams& p, int dtype, int32_t* status,
+                                       hipStream_t s);
+hipError_t launch_ingress_finalize(const IngressParams& p, hipStream_t s);
+hipError_t launch_reset_fail(DeviceState* st, hipStream_t s);
+hipError_t launch_chacha_xor(const uint8_t* src, uint8_t* dst, size_t len, ChaKey key,
+                             uint32_t ctr, uint32_t n0, uint32_t n1, uint32_t n2, hipStream_t s);
+hipError_t launch_siphash(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
+                          uint8_t* tag, hipStream_t s);
+
+}  // namespace ztcp

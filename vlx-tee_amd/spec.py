@@ -1,0 +1,115 @@
+"""Wire-format constants and payload sizing of a cold page.
+
+Mirror of research/baseline_codec/cold_page_spec.py (spec:47-67, spec:117-161,
+spec:164-253): the 32-byte little-endian header, presets, RoPE modes and the
+payload size (padded to 4 bytes) the reference's Python wrapper passes as
+``expected_payload_bytes``.
+"""
+from __future__ import annotations
+
+import enum
+import struct
+from dataclasses import dataclass
+
+MAGIC_ZTCP = 0x5A54
+CODEC_VERSION = 1
+HEADER_BYTES = 32
+TAG_BYTES = 16
+HEADER_STRUCT = struct.Struct("<HBBIIHHQQ")
+
+
+class QuantPreset(enum.IntEnum):
+    INT4_SYM = 1
+    K8V4_ASYM = 2
+    FP8_ONLY = 3
+
+
+class RoPEMode(enum.IntEnum):
+    QUANTIZE_ALL = 0
+    PRESERVE_FP8 = 1
+    PRESERVE_RAW = 2
+
+
+def pack_header(preset: int, rope_mode: int, tenant_id_hash: int, model_id_hash: int,
+                layer_id: int, head_group_id: int, page_token_hash: int,
+                sequence_nonce: int) -> bytes:
+    flags = (int(preset) & 0x0F) | ((int(rope_mode) & 0x0F) << 4)
+    return HEADER_STRUCT.pack(MAGIC_ZTCP, CODEC_VERSION, flags, tenant_id_hash & 0xFFFFFFFF,
+                              model_id_hash & 0xFFFFFFFF, layer_id & 0xFFFF,
+                              head_group_id & 0xFFFF, page_token_hash & (2**64 - 1),
+                              sequence_nonce & (2**64 - 1))
+
+
+def unpack_header(b: bytes) -> dict:
+    magic, version, flags, tenant, model, layer, hg, tok, seq = HEADER_STRUCT.unpack(b[:HEADER_BYTES])
+    return dict(magic=magic, version=version, preset=flags & 0x0F, rope_mode=flags >> 4,
+                tenant_id_hash=tenant, model_id_hash=model, layer_id=layer, head_group_id=hg,
+                page_token_hash=tok, sequence_nonce=seq)
+
+
+@dataclass(frozen=True)
+class ColdPageGeometry:
+    num_tokens: int = 64
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    rope_dim: int = 64
+    group_size: int = 16
+    hot_element_bytes: int = 2
+    is_mla_single_buffer: bool = False
+
+    def __post_init__(self) -> None:
+        if self.group_size != 16:
+            raise ValueError("the wire format fixes group_size = 16 (cpp:1126)")
+        if self.head_dim % 16 or self.head_dim < 16:
+            raise ValueError("head_dim must be a positive multiple of 16")
+        if self.rope_dim < 0 or self.rope_dim > self.head_dim or self.rope_dim % 16:
+            raise ValueError("Invalid rope_dim")
+
+    @property
+    def vectors_per_buffer(self) -> int:
+        return self.num_tokens * self.num_kv_heads
+
+    @property
+    def hot_page_bytes(self) -> int:
+        buffers = 1 if self.is_mla_single_buffer else 2
+        return buffers * self.vectors_per_buffer * self.head_dim * self.hot_element_bytes
+
+    def required_payload_bytes(self, preset: int, rope_mode: int) -> int:
+        """Unpadded payload (cpp:1439-1474)."""
+        if preset not in (1, 2, 3) or rope_mode not in (0, 1, 2):
+            raise ValueError("Invalid preset or rope_mode")
+        vecs, D, R = self.vectors_per_buffer, self.head_dim, self.rope_dim
+        req = 0
+        if rope_mode == 2 and R > 0:
+            req += vecs * R * 2
+        elif rope_mode == 1 and R > 0:
+            req += vecs * R + vecs * (R // 16) * 2
+        kq = D if rope_mode == 0 else D - R
+        if kq > 0:
+            req += (vecs * (kq // 2) if preset == 1 else vecs * kq) + vecs * (kq // 16) * 2
+        if not self.is_mla_single_buffer:
+            req += (vecs * (D // 2) if preset in (1, 2) else vecs * D) + vecs * (D // 16) * 2
+        return req
+
+    def payload_bytes(self, preset: int, rope_mode: int) -> int:
+        """Payload padded to a 4-byte boundary (spec:244-246)."""
+        r = self.required_payload_bytes(preset, rope_mode)
+        return (r + 3) & ~3
+
+    def cold_blob_bytes(self, preset: int, rope_mode: int) -> int:
+        return HEADER_BYTES + self.payload_bytes(preset, rope_mode) + TAG_BYTES
+
+
+def hash32(text: str) -> int:
+    """32-bit domain identifier hash (spec:70-74): BLAKE2s-32, little-endian."""
+    import hashlib
+
+    return int.from_bytes(hashlib.blake2s(text.encode("utf-8"), digest_size=4).digest(), "little")
+
+
+def hash64_tokens(token_ids) -> int:
+    """64-bit token-id hash of a page (spec:77-80): BLAKE2s-64 over LE int32."""
+    import hashlib
+
+    buf = struct.pack(f"<{len(token_ids)}i", *token_ids)
+    return int.from_bytes(hashlib.blake2s(buf, digest_size=8).digest(), "little")
