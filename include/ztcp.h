@@ -168,6 +168,15 @@ int ztcp_chacha20_xor(const uint8_t* src, uint8_t* dst, size_t len, const uint8_
 int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
                     uint8_t* tag16, void* stream);
 
+/* Self-check of the device arithmetic the fused quantizer relies on: for
+ * every amax the FP16 and BF16 hot dtypes can produce, the fast scale (a
+ * corrected quotient) equals fp16(amax / 127) and fp16(amax / 7) by IEEE
+ * division whenever it is a normal fp16 value, and the Newton-refined
+ * reciprocal equals 1 / s for every positive finite fp16 scale.  Returns the
+ * number of violations (0 = pass) or a negative error.  A test hook like the
+ * reference's (cpp:2499-2538); it has no counterpart of its own there. */
+int ztcp_selftest(void);
+
 /* Device-side diagnostics of the current device: returns and clears the
  * sticky flags a kernel's bounded waits set (0 = none). Synchronizes. */
 int ztcp_device_diag(void);

@@ -279,3 +279,8 @@ def test_kat_hooks_on_gpu(hip, O):
                                           torch.from_numpy(nb))
             assert ct.cpu().numpy().tobytes() == O.chacha20_xor(data.tobytes(), kb.tobytes(), 3,
                                                                 nb.tobytes())
+
+
+def test_fast_quantizer_arithmetic_selftest(hip):
+    """Exhaustive device check of the fast scale / reciprocal (ztcp_selftest)."""
+    assert hip.N.lib().ztcp_selftest() == 0

@@ -25,7 +25,7 @@ EXPORTS = (
     "ztcp_egress_peak_into", "ztcp_egress_batch",
     "ztcp_ingress_peak_into", "ztcp_ingress_batch",
     "ztcp_chacha20_xor", "ztcp_siphash128",
-    "ztcp_device_diag", "ztcp_strerror",
+    "ztcp_selftest", "ztcp_device_diag", "ztcp_strerror",
 )
 
 
@@ -82,6 +82,8 @@ def lib() -> C.CDLL:
     L.ztcp_chacha20_xor.restype = i32
     L.ztcp_siphash128.argtypes = [P, C.c_size_t, u64, u64, P, P]
     L.ztcp_siphash128.restype = i32
+    L.ztcp_selftest.argtypes = []
+    L.ztcp_selftest.restype = i32
     L.ztcp_device_diag.argtypes = []
     L.ztcp_device_diag.restype = i32
     L.ztcp_strerror.argtypes = [i32]

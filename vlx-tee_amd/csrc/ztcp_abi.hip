@@ -15,7 +15,6 @@ using namespace ztcp;
 
 namespace {
 
-constexpr int kWaves = 16;          // 1 MAC wave + 15 producer waves
 constexpr int kMaxBatchFlags = 4096;
 
 struct DeviceCtx {
@@ -149,11 +148,21 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
     p.ppw = pages_per_group(batch, ctx->cu_count);
     p.n_batches = (p.ppw * lay.n_units + 63) / 64;
     p.state = ctx->state;
+    // MAC order of the payload: each section's codes (gated per unit), then its scales
+    p.n_seg = 0;
+    p.mac_chunks = 0;
+    for (int si = 0; si < lay.n_sec; ++si) {
+        const Section& s = lay.sec[si];
+        const uint32_t bpg = (uint32_t)code_bytes_per_group(s.kind);
+        p.seg[p.n_seg++] = MacSeg{s.q_off, (uint32_t)s.n_groups * bpg / 64u, s.unit_begin, (int32_t)(bpg / 2u)};
+        if (s.kind != kSecRaw) p.seg[p.n_seg++] = MacSeg{s.s_off, (uint32_t)s.n_units, s.unit_begin, 0};
+    }
+    for (int i = 0; i < p.n_seg; ++i) p.mac_chunks += p.seg[i].n;
 
     const bool fast = lay.aligned && expected_payload == (int64_t)lay.required && blob_bytes % 16 == 0 &&
                       p.n_batches <= kMaxBatchFlags &&
                       (descs || (aligned16(k) && aligned16(v) && aligned16(blobs)));
-    hipError_t e = fast ? launch_egress_fused(p, g->hot_dtype, kWaves, stream)
+    hipError_t e = fast ? launch_egress_fused(p, g->hot_dtype, stream)
                         : launch_egress_generic(p, g->hot_dtype, stream);
     return e == hipSuccess ? ZTCP_OK : ZTCP_EHIP;
 }
@@ -224,7 +233,7 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
         if (fast) {
             p.n_units = units;
             p.n_batches = (p.ppw * units + 63) / 64;
-            e = launch_ingress_fused(p, g->hot_dtype, kWaves, stream);
+            e = launch_ingress_fused(p, g->hot_dtype, stream);
             if (e == hipSuccess && !p.per_page) e = launch_ingress_finalize(p, stream);
         } else {
             p.n_units = (int32_t)(vecs * (g->head_dim / 16) * (mla ? 1 : 2));  // groups per page
@@ -331,6 +340,19 @@ int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
     if (!tag16 || (len && !data)) return ZTCP_EINVAL;
     return launch_siphash(data, len, mk0, mk1, tag16, (hipStream_t)stream) == hipSuccess ? ZTCP_OK
                                                                                        : ZTCP_EHIP;
+}
+
+int ztcp_selftest(void) {
+    unsigned int* bad = nullptr;
+    if (hipMalloc(&bad, sizeof(unsigned int)) != hipSuccess) return ZTCP_EHIP;
+    unsigned int h = 0;
+    int rc = ZTCP_OK;
+    if (hipMemcpy(bad, &h, sizeof h, hipMemcpyHostToDevice) != hipSuccess ||
+        launch_selftest(bad, nullptr) != hipSuccess ||
+        hipMemcpy(&h, bad, sizeof h, hipMemcpyDeviceToHost) != hipSuccess)
+        rc = ZTCP_EHIP;
+    (void)hipFree(bad);
+    return rc == ZTCP_OK ? (int)h : rc;
 }
 
 int ztcp_device_diag(void) {

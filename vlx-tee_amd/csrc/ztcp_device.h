@@ -71,49 +71,84 @@ __device__ __forceinline__ void chacha_block(const ChaKey& key, uint32_t ctr, ui
 }
 
 // ---------------------------------------------------------------------------
-// SipHash-2-4 with 128-bit output (cpp:401-471).
+// SipHash-2-4 with 128-bit output (cpp:401-471), on 32-bit halves.
+// Each 64-bit state word is a (lo, hi) pair of 32-bit registers: a 64-bit add
+// is add-with-carry, a rotate by n < 32 is two v_alignbit_b32, and the rotate
+// by 32 is a free exchange of the halves, so no register-pair fix-ups are
+// needed.  One page per lane; the chain is strictly sequential.
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ uint64_t rotl64(uint64_t x, int n) {
-    return (x << n) | (x >> (64 - n));
-}
-
 struct Sip {
-    uint64_t v0, v1, v2, v3;
+    uint32_t a0, a1, b0, b1, c0, c1, d0, d1;  // v0 = (a1:a0), v1 = (b1:b0), v2 = (c1:c0), v3 = (d1:d0)
 
+    __device__ __forceinline__ static void add(uint32_t& lo, uint32_t& hi, uint32_t blo, uint32_t bhi) {
+        unsigned int carry;
+        lo = __builtin_addc(lo, blo, 0u, &carry);
+        hi = __builtin_addc(hi, bhi, carry, &carry);
+    }
+    __device__ __forceinline__ static void rot(uint32_t& lo, uint32_t& hi, int n) {  // 0 < n < 32
+        const uint32_t nl = __builtin_amdgcn_alignbit(lo, hi, 32 - n);
+        const uint32_t nh = __builtin_amdgcn_alignbit(hi, lo, 32 - n);
+        lo = nl;
+        hi = nh;
+    }
     __device__ __forceinline__ void init(uint64_t mk0, uint64_t mk1) {
-        v0 = 0x736F6D6570736575ull ^ mk0;
-        v1 = 0x646F72616E646F6Dull ^ mk1 ^ 0xEEull;
-        v2 = 0x6C7967656E657261ull ^ mk0;
-        v3 = 0x7465646279746573ull ^ mk1;
+        const uint64_t v0 = 0x736F6D6570736575ull ^ mk0, v1 = 0x646F72616E646F6Dull ^ mk1 ^ 0xEEull;
+        const uint64_t v2 = 0x6C7967656E657261ull ^ mk0, v3 = 0x7465646279746573ull ^ mk1;
+        a0 = (uint32_t)v0; a1 = (uint32_t)(v0 >> 32);
+        b0 = (uint32_t)v1; b1 = (uint32_t)(v1 >> 32);
+        c0 = (uint32_t)v2; c1 = (uint32_t)(v2 >> 32);
+        d0 = (uint32_t)v3; d1 = (uint32_t)(v3 >> 32);
     }
     __device__ __forceinline__ void round() {
-        v0 += v1; v1 = rotl64(v1, 13); v1 ^= v0; v0 = rotl64(v0, 32);
-        v2 += v3; v3 = rotl64(v3, 16); v3 ^= v2;
-        v0 += v3; v3 = rotl64(v3, 21); v3 ^= v0;
-        v2 += v1; v1 = rotl64(v1, 17); v1 ^= v2; v2 = rotl64(v2, 32);
+        add(a0, a1, b0, b1); rot(b0, b1, 13); b0 ^= a0; b1 ^= a1;
+        { const uint32_t t = a0; a0 = a1; a1 = t; }
+        add(c0, c1, d0, d1); rot(d0, d1, 16); d0 ^= c0; d1 ^= c1;
+        add(a0, a1, d0, d1); rot(d0, d1, 21); d0 ^= a0; d1 ^= a1;
+        add(c0, c1, b0, b1); rot(b0, b1, 17); b0 ^= c0; b1 ^= c1;
+        { const uint32_t t = c0; c0 = c1; c1 = t; }
     }
-    __device__ __forceinline__ void absorb(uint64_t m) {
-        v3 ^= m;
+    __device__ __forceinline__ void absorb(uint32_t mlo, uint32_t mhi) {
+        d0 ^= mlo; d1 ^= mhi;
         round();
         round();
-        v0 ^= m;
+        a0 ^= mlo; a1 ^= mhi;
+    }
+    __device__ __forceinline__ void absorb(uint64_t m) { absorb((uint32_t)m, (uint32_t)(m >> 32)); }
+    __device__ __forceinline__ void absorb(uint4 q) {  // two little-endian words
+        absorb(q.x, q.y);
+        absorb(q.z, q.w);
     }
     // Final word = (total_len & 0xff) << 56 | tail bytes (cpp:458-470), then
     // the 128-bit finalization (cpp:447-456).
     __device__ __forceinline__ void finish(uint64_t last_word, uint64_t& lo, uint64_t& hi) {
         absorb(last_word);
-        v2 ^= 0xEEull;
+        c0 ^= 0xEEu;
         round(); round(); round(); round();
-        lo = v0 ^ v1 ^ v2 ^ v3;
-        v1 ^= 0xDDull;
+        lo = ((uint64_t)(a1 ^ b1 ^ c1 ^ d1) << 32) | (a0 ^ b0 ^ c0 ^ d0);
+        b0 ^= 0xDDu;
         round(); round(); round(); round();
-        hi = v0 ^ v1 ^ v2 ^ v3;
+        hi = ((uint64_t)(a1 ^ b1 ^ c1 ^ d1) << 32) | (a0 ^ b0 ^ c0 ^ d0);
     }
 };
 
 __device__ __forceinline__ uint64_t lo64(uint4 a) { return (uint64_t)a.x | ((uint64_t)a.y << 32); }
 __device__ __forceinline__ uint64_t hi64(uint4 a) { return (uint64_t)a.z | ((uint64_t)a.w << 32); }
+
+// 16-byte global loads and stores through global-address-space pointers:
+// they stay on the global_* path (in-order vmcnt accounting, so a prefetched
+// load is not waited for together with newer ones) instead of flat_*.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4* gptr_ro;
+typedef __attribute__((address_space(1))) u32x4* gptr_rw;
+
+__device__ __forceinline__ uint4 ldg16(const void* p, int64_t i = 0) {
+    const u32x4 v = ((gptr_ro)p)[i];
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void stg16(void* p, int64_t i, uint4 x) {
+    ((gptr_rw)p)[i] = u32x4{x.x, x.y, x.z, x.w};
+}
 
 // ---------------------------------------------------------------------------
 // Hot dtype conversions.
@@ -154,69 +189,92 @@ __device__ __forceinline__ uint32_t pack_hot(float lo, float hi) {
 //        q = clamp(int(nearbyintf(v * inv) + 8), 0, 15); byte i = q[2i] | q[2i+1] << 4
 // Input: a group as 8 words (element 2i in the low half of word i).
 //
-// Fast path: for finite inputs and a nonzero scale, |v * inv| is bounded
-// (<= 190), so clamp-then-round equals round-then-clamp, and adding 1.5*2^23
-// (+8 for int4) rounds to nearest-even in the same fp32 add: the low bits of
-// the sum are the code.  Groups holding NaN / inf, or an int8 scale that
-// underflows to 0 (amax <= 3.79e-6), take the exact emulation of the x86
-// conversions instead (NaN -> 0 after the int conversion).
+// Fast path (every group whose scale is a normal fp16 number and whose
+// elements are finite):
+//   * s is computed as q0 = amax * (1/C), q = fma(fma(-q0, C, amax), 1/C, q0)
+//     (a corrected quotient) and inv as a Newton-refined v_rcp_f32.  Both are
+//     checked exhaustively against correctly rounded division
+//     (ztcp_selftest): the reciprocal equals 1/s for every positive finite
+//     fp16 s, and fp16(q) equals fp16(amax / C) for every amax the fp16 and
+//     bf16 hot dtypes can produce whenever the result is a normal fp16 value.
+//   * with a normal s, |v * inv| <= C * (1 + 2^-10) < C + 0.5, so no clamp is
+//     needed, and adding 1.5 * 2^23 (+8 for int4) rounds to nearest-even in
+//     that same fp32 add: the low bits of the sum are the code.
+// Every other group (NaN / inf elements, a zero, subnormal or infinite
+// scale) takes the exact emulation: IEEE division and the x86 conversions
+// (NaN -> 0 after the int conversion), identical to the reference.
 // ---------------------------------------------------------------------------
 
-template <int DT>
-__device__ __forceinline__ uint32_t group_amax_bits(const uint32_t w[8]) {
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
-#pragma unroll
-    for (int i = 1; i < 8; ++i)
-        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
-    return m.x > m.y ? m.x : m.y;
-}
+struct GroupCodes {
+    uint32_t q0, q1, q2, q3;  // code words (int4 uses q0, q1)
+    uint32_t scale;           // fp16 scale bits
+};
 
-template <int DT>
-__device__ __forceinline__ float bits_to_f32(uint32_t b) {
-    if constexpr (DT == kHotBf16) return __uint_as_float(b << 16);
-    else return f16_to_f32(b);
-}
-
-// Scale bits and reciprocal for a group; returns true for the exact path.
+// Exact emulation of the reference for one group; words by value so the
+// fast path's registers never have to be spilled for this rare call.
 template <int DT, int BITS>
-__device__ __forceinline__ bool group_scale(const uint32_t w[8], uint32_t& scale_bits,
-                                            float& inv) {
-    const uint32_t ab = group_amax_bits<DT>(w);
-    const uint32_t inf_bits = DT == kHotBf16 ? 0x7F80u : 0x7C00u;
-    const float amax_v = bits_to_f32<DT>(ab);
-    const float amax = amax_v > 1e-6f ? amax_v : 1e-6f;
-    scale_bits = f32_to_f16(amax / (BITS == 8 ? 127.0f : 7.0f));
-    inv = 1.0f / f16_to_f32(scale_bits);
-    return ab >= inf_bits || scale_bits == 0;
-}
-
-// Exact amax for groups that hold NaN (the reference skips NaN: `av > amax`).
-template <int DT, int BITS>
-__device__ __noinline__ void group_scale_exact(const uint32_t w[8], uint32_t& scale_bits,
-                                               float& inv) {
+__device__ __noinline__ GroupCodes quant_group_exact(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                     uint32_t w4, uint32_t w5, uint32_t w6, uint32_t w7) {
+    const uint32_t w[8] = {w0, w1, w2, w3, w4, w5, w6, w7};
     float amax = 1e-6f;
+#pragma unroll
     for (int i = 0; i < 8; ++i) {
-        float a = fabsf(hot_lo<DT>(w[i]));
-        float b = fabsf(hot_hi<DT>(w[i]));
+        const float a = fabsf(hot_lo<DT>(w[i]));
+        const float b = fabsf(hot_hi<DT>(w[i]));
         if (a > amax) amax = a;
         if (b > amax) amax = b;
     }
-    scale_bits = f32_to_f16(amax / (BITS == 8 ? 127.0f : 7.0f));
-    inv = 1.0f / f16_to_f32(scale_bits);
+    GroupCodes r;
+    r.scale = f32_to_f16(amax / (BITS == 8 ? 127.0f : 7.0f));
+    const float inv = 1.0f / f16_to_f32(r.scale);
+    uint32_t q[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < (BITS == 8 ? 4 : 2); ++j) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (BITS == 8) {
+                const uint32_t e = w[2 * j + (i >> 1)];
+                const float v = (i & 1) ? hot_hi<DT>(e) : hot_lo<DT>(e);
+                float rr = rintf(v * inv);
+                if (rr < -127.0f) rr = -127.0f;
+                if (rr > 127.0f) rr = 127.0f;
+                const uint32_t c = rr != rr ? 0u : ((uint32_t)(int)rr & 0xFFu);
+                word |= c << (8 * i);
+            } else {
+                const uint32_t e = w[4 * j + i];
+                uint32_t nib[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float v = h ? hot_hi<DT>(e) : hot_lo<DT>(e);
+                    const float rr = rintf(v * inv) + 8.0f;
+                    int u = rr != rr ? INT32_MIN : (int)rr;
+                    nib[h] = (uint32_t)(u < 0 ? 0 : (u > 15 ? 15 : u));
+                }
+                word |= (nib[0] | (nib[1] << 4)) << (8 * i);
+            }
+        }
+        q[j] = word;
+    }
+    r.q0 = q[0]; r.q1 = q[1]; r.q2 = q[2]; r.q3 = q[3];
+    return r;
 }
 
-__device__ __forceinline__ uint32_t code8_exact(float y) {
-    float r = rintf(y);
-    if (r < -127.0f) r = -127.0f;
-    if (r > 127.0f) r = 127.0f;
-    return r != r ? 0u : ((uint32_t)(int)r & 0xFFu);
+// fp16(amax / C) for the fast path (see above); valid when the result is normal.
+template <int BITS>
+__device__ __forceinline__ uint32_t scale_fast(float amax) {
+    constexpr float C = BITS == 8 ? 127.0f : 7.0f;
+    constexpr float rC = BITS == 8 ? (1.0f / 127.0f) : (1.0f / 7.0f);
+    const float q0 = amax * rC;
+    const float r = __builtin_fmaf(-q0, C, amax);
+    return f32_to_f16(__builtin_fmaf(r, rC, q0));
 }
-__device__ __forceinline__ uint32_t code4_exact(float y) {
-    float r = rintf(y) + 8.0f;
-    int u = r != r ? INT32_MIN : (int)r;
-    u = u < 0 ? 0 : (u > 15 ? 15 : u);
-    return (uint32_t)u;
+
+// 1 / s for a positive finite fp16 value s: Newton-refined v_rcp_f32.
+__device__ __forceinline__ float recip_fast(float s) {
+    const float r0 = __builtin_amdgcn_rcpf(s);
+    const float e = __builtin_fmaf(-s, r0, 1.0f);
+    return __builtin_fmaf(e, r0, r0);
 }
 
 // Pack byte 0 of four words into one word.
@@ -226,64 +284,61 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint3
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
-// int8: 16 elements -> 4 code words; returns the fp16 scale bits.
-template <int DT>
-__device__ __forceinline__ uint32_t quant_group_int8(const uint32_t w[8], uint32_t q[4]) {
-    uint32_t sb;
-    float inv;
-    if (!group_scale<DT, 8>(w, sb, inv)) {
+// One group: CW code words (4 for int8, 2 for int4); returns the fp16 scale bits.
+template <int DT, int BITS>
+__device__ __forceinline__ uint32_t quant_group(const uint32_t w[8], uint32_t q[4]) {
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        f[2 * i] = hot_lo<DT>(w[i]);
+        f[2 * i + 1] = hot_hi<DT>(w[i]);
+    }
+    // amax (NaN-free groups: max3 over |f| equals the reference's compare loop)
+    float m0 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[0]), fabsf(f[1])), fabsf(f[2]));
+    float m1 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[3]), fabsf(f[4])), fabsf(f[5]));
+    float m2 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[6]), fabsf(f[7])), fabsf(f[8]));
+    float m3 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[9]), fabsf(f[10])), fabsf(f[11]));
+    float m4 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[12]), fabsf(f[13])), fabsf(f[14]));
+    m0 = __builtin_fmaxf(__builtin_fmaxf(m0, m1), m2);
+    m3 = __builtin_fmaxf(__builtin_fmaxf(m3, m4), fabsf(f[15]));
+    const float amax = __builtin_fmaxf(__builtin_fmaxf(m0, m3), 1e-6f);
+    const uint32_t sb = scale_fast<BITS>(amax);
+    // exact path: NaN / inf elements (amax not < inf), scale zero / subnormal / inf
+    const bool special = !(amax < __builtin_inff()) || (sb - 0x0400u) >= (0x7C00u - 0x0400u);
+    if (__builtin_expect(special, 0)) {
+        const GroupCodes r = quant_group_exact<DT, BITS>(w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]);
+        q[0] = r.q0; q[1] = r.q1; q[2] = r.q2; q[3] = r.q3;
+        return r.scale;
+    }
+    const float inv = recip_fast(f16_to_f32(sb));
+    if constexpr (BITS == 8) {
         uint32_t t[16];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float a = __builtin_amdgcn_fmed3f(hot_lo<DT>(w[i]) * inv, -127.0f, 127.0f);
-            float b = __builtin_amdgcn_fmed3f(hot_hi<DT>(w[i]) * inv, -127.0f, 127.0f);
-            t[2 * i] = __float_as_uint(a + 12582912.0f);
-            t[2 * i + 1] = __float_as_uint(b + 12582912.0f);
-        }
+        for (int i = 0; i < 16; ++i) t[i] = __float_as_uint(f[i] * inv + 12582912.0f);
 #pragma unroll
         for (int j = 0; j < 4; ++j) q[j] = pack_low_bytes(t[4 * j], t[4 * j + 1], t[4 * j + 2], t[4 * j + 3]);
-        return sb;
-    }
-    group_scale_exact<DT, 8>(w, sb, inv);
-    for (int j = 0; j < 4; ++j) {
-        uint32_t c0 = code8_exact(hot_lo<DT>(w[2 * j]) * inv);
-        uint32_t c1 = code8_exact(hot_hi<DT>(w[2 * j]) * inv);
-        uint32_t c2 = code8_exact(hot_lo<DT>(w[2 * j + 1]) * inv);
-        uint32_t c3 = code8_exact(hot_hi<DT>(w[2 * j + 1]) * inv);
-        q[j] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    } else {
+        uint32_t b[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)  // bits 0..3 of each sum hold q + 8; bits 4..7 are zero
+            b[i] = (__float_as_uint(f[2 * i + 1] * inv + 12582920.0f) << 4) |
+                   __float_as_uint(f[2 * i] * inv + 12582920.0f);
+        q[0] = pack_low_bytes(b[0], b[1], b[2], b[3]);
+        q[1] = pack_low_bytes(b[4], b[5], b[6], b[7]);
     }
     return sb;
 }
 
-// int4: 16 elements -> 2 code words; returns the fp16 scale bits.
+template <int DT>
+__device__ __forceinline__ uint32_t quant_group_int8(const uint32_t w[8], uint32_t q[4]) {
+    return quant_group<DT, 8>(w, q);
+}
 template <int DT>
 __device__ __forceinline__ uint32_t quant_group_int4(const uint32_t w[8], uint32_t q[2]) {
-    uint32_t sb;
-    float inv;
-    if (!group_scale<DT, 4>(w, sb, inv)) {
-        uint32_t b[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float lo = __builtin_amdgcn_fmed3f(hot_lo<DT>(w[i]) * inv, -8.0f, 7.0f);
-            float hi = __builtin_amdgcn_fmed3f(hot_hi<DT>(w[i]) * inv, -8.0f, 7.0f);
-            // bits 0..3 of each sum hold q + 8; bits 4..7 are zero.
-            b[i] = (__float_as_uint(hi + 12582920.0f) << 4) | __float_as_uint(lo + 12582920.0f);
-        }
-        q[0] = pack_low_bytes(b[0], b[1], b[2], b[3]);
-        q[1] = pack_low_bytes(b[4], b[5], b[6], b[7]);
-        return sb;
-    }
-    group_scale_exact<DT, 4>(w, sb, inv);
-    for (int j = 0; j < 2; ++j) {
-        uint32_t word = 0;
-        for (int i = 0; i < 4; ++i) {
-            uint32_t e = w[4 * j + i];
-            uint32_t lo = code4_exact(hot_lo<DT>(e) * inv);
-            uint32_t hi = code4_exact(hot_hi<DT>(e) * inv);
-            word |= (lo | (hi << 4)) << (8 * i);
-        }
-        q[j] = word;
-    }
+    uint32_t t[4];
+    const uint32_t sb = quant_group<DT, 4>(w, t);
+    q[0] = t[0];
+    q[1] = t[1];
     return sb;
 }
 

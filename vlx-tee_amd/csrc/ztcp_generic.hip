@@ -274,6 +274,35 @@ __global__ void siphash_kernel(const uint8_t* data, uint64_t len, uint64_t mk0, 
     }
 }
 
+// ---- self-test of the fast quantizer arithmetic -------------------------------
+// Thread i covers magnitude bits i of both hot dtypes (amax candidates) and,
+// for i < 0x7C00, the fp16 scale with bits i (reciprocal candidates).
+// Violations: a fast scale that is a normal fp16 value but differs from
+// fp16(amax / C) by IEEE division, or a fast reciprocal that differs from 1 / s.
+__global__ void selftest_kernel(unsigned int* bad) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 0x8000u) return;
+    uint32_t n = 0;
+    const float cand[2] = {__uint_as_float(i << 16), f16_to_f32(i)};
+    for (int d = 0; d < 2; ++d) {
+        const float a = cand[d] > 1e-6f ? cand[d] : 1e-6f;
+        if (!(a < __builtin_inff())) continue;
+        const uint32_t f8 = scale_fast<8>(a), f4 = scale_fast<4>(a);
+        if (f8 >= 0x0400u && f8 < 0x7C00u && f8 != f32_to_f16(a / 127.0f)) ++n;
+        if (f4 >= 0x0400u && f4 < 0x7C00u && f4 != f32_to_f16(a / 7.0f)) ++n;
+    }
+    if (i > 0 && i < 0x7C00u) {
+        const float sv = f16_to_f32(i);
+        if (__float_as_uint(recip_fast(sv)) != __float_as_uint(1.0f / sv)) ++n;
+    }
+    if (n) atomicAdd(bad, n);
+}
+
+hipError_t launch_selftest(unsigned int* bad, hipStream_t s) {
+    hipLaunchKernelGGL(selftest_kernel, dim3(0x8000 / 256), dim3(256), 0, s, bad);
+    return hipGetLastError();
+}
+
 // ---- launchers ---------------------------------------------------------------
 
 static uint32_t grid_for(int64_t items, int block, int64_t cap = 65536) {

@@ -3,12 +3,13 @@
 // HBM read of the blob and one HBM write of the hot page.  Replaces the
 // per-page decoder of fused_decode_cold_pages_peak_into_cpu (cpp:2309-2463).
 //
-// One workgroup handles up to 64 pages with 16 waves:
+// One workgroup handles up to 64 pages with 12 waves:
 //   * wave 0 verifies one page per lane: magic/version (status 1), AAD
 //     tenant/model/layer/token hash (status 2), the SipHash-2-4-128 tag over
 //     header || ciphertext (status 3), then flags and payload size (status 1),
 //     in the reference's order (cpp:2313-2355).
-//   * waves 1..15 decrypt and dequantize (page, unit) items concurrently,
+//   * waves on the other three SIMDs decrypt and dequantize (page, unit)
+//     items concurrently (waves 4 and 8 share the verify wave's SIMD and exit),
 //     each page according to its own header flags.  This is speculative: a
 //     page whose verdict is not OK has its outputs zeroed before the kernel
 //     ends (per-page mode) or by the finalize kernel (all-or-nothing mode,
@@ -26,27 +27,17 @@ __device__ __forceinline__ void xor_block(uint32_t ct[16], const uint32_t ks[16]
 }
 
 __device__ __forceinline__ void load_block(const uint8_t* p, uint32_t w[16]) {
-    const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint4 a = q[i];
+        const uint4 a = ldg16(p, i);
         w[4 * i] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
     }
 }
 
 __device__ __forceinline__ void store_group(uint8_t* p, const uint32_t o[8]) {
-    uint4* q = reinterpret_cast<uint4*>(p);
-    q[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    q[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    stg16(p, 0, make_uint4(o[0], o[1], o[2], o[3]));
+    stg16(p, 1, make_uint4(o[4], o[5], o[6], o[7]));
 }
-
-struct Cursor {
-    int64_t vec;
-    int32_t g;
-    __device__ __forceinline__ void step(int32_t gpv) {
-        if (++g == gpv) { g = 0; ++vec; }
-    }
-};
 
 template <int DT, int KIND>
 __device__ __forceinline__ void decode_quant_unit(const IngressParams& p, const uint8_t* pay,
@@ -57,8 +48,8 @@ __device__ __forceinline__ void decode_quant_unit(const IngressParams& p, const 
     constexpr int NBLK = 32 / GPB;
     constexpr int CW = KIND == kSecInt8 ? 4 : 2;
     const int32_t G0 = lu * 32;
-    Cursor cur{G0 / gpv, G0 % gpv};
-    const int64_t row = (int64_t)p.head_dim * 2;
+    GroupCursor cur = group_cursor(G0, gpv, col, p.head_dim);
+    const uint32_t skip = (uint32_t)(p.head_dim - gpv * 16) * 2u;
     const uint32_t s_unit = s_off + (uint32_t)lu * 64u;
     uint32_t sc[16];
     load_block(pay + s_unit, sc);
@@ -78,8 +69,8 @@ __device__ __forceinline__ void decode_quant_unit(const IngressParams& p, const 
             uint32_t o[8];
             if constexpr (KIND == kSecInt8) dequant_group_int8<DT>(ct + 4 * i, sbits, o);
             else dequant_group_int4<DT>(ct + 2 * i, sbits, o);
-            store_group(out + cur.vec * row + (int64_t)(col + cur.g * 16) * 2, o);
-            cur.step(gpv);
+            store_group(out + cur.off, o);
+            cur.step(gpv, skip);
         }
         // consume this block's scales
 #pragma unroll
@@ -92,8 +83,8 @@ __device__ __forceinline__ void decode_raw_unit(const IngressParams& p, const ui
                                                 int32_t col, uint32_t q_off, uint32_t n0,
                                                 uint32_t n1, uint32_t n2) {
     const int32_t G0 = lu * 32;
-    Cursor cur{G0 / gpv, G0 % gpv};
-    const int64_t row = (int64_t)p.head_dim * 2;
+    GroupCursor cur = group_cursor(G0, gpv, col, p.head_dim);
+    const uint32_t skip = (uint32_t)(p.head_dim - gpv * 16) * 2u;
     const uint32_t code0 = q_off + (uint32_t)G0 * 32u;
 #pragma unroll 1
     for (int j = 0; j < 16; ++j) {
@@ -101,10 +92,10 @@ __device__ __forceinline__ void decode_raw_unit(const IngressParams& p, const ui
         load_block(pay + code0 + (uint32_t)j * 64u, ct);
         chacha_block(p.key, 1u + code0 / 64u + (uint32_t)j, n0, n1, n2, ks);
         xor_block(ct, ks);
-        store_group(out + cur.vec * row + (int64_t)(col + cur.g * 16) * 2, ct);
-        cur.step(gpv);
-        store_group(out + cur.vec * row + (int64_t)(col + cur.g * 16) * 2, ct + 8);
-        cur.step(gpv);
+        store_group(out + cur.off, ct);
+        cur.step(gpv, skip);
+        store_group(out + cur.off, ct + 8);
+        cur.step(gpv, skip);
     }
 }
 
@@ -129,40 +120,37 @@ __device__ void decode_unit(const IngressParams& p, const Layout& lay, int64_t p
         decode_raw_unit(p, pay, out, lu, gpv, col, q_off, n0, n1, n2);
 }
 
-// Verdict of one page (cpp:2313-2355); the MAC covers header || payload.
+// Verdict of one page (cpp:2313-2355); the MAC covers header || payload,
+// read one 64-byte chunk ahead of the chunk being absorbed.
 __device__ int32_t verify_page(const IngressParams& p, int64_t page) {
     const uint8_t* blob = ingress_blob(p, page);
-    const uint4* q = reinterpret_cast<const uint4*>(blob);
-    const uint4 h0 = q[0], h1 = q[1];
+    const uint4 h0 = ldg16(blob, 0), h1 = ldg16(blob, 1);
     Sip s;
     s.init(p.mk0, p.mk1);
-    s.absorb(lo64(h0)); s.absorb(hi64(h0));
-    s.absorb(lo64(h1)); s.absorb(hi64(h1));
-    const int n16 = (int)(p.payload / 16u);  // payload % 16 == 0 on this path
-    const uint4* c = q + 2;
-    const int n64 = n16 / 4;
-    if (n64 > 0) {
-        uint4 a0 = c[0], a1 = c[1], a2 = c[2], a3 = c[3];
+    // header || payload = n16 16-byte words (payload % 16 == 0 on this path)
+    const uint32_t n16 = (kHeader + p.payload) / 16u;
+    const uint32_t n64 = n16 / 4u;
+    uint4 a[4], b[4];
+    a[0] = h0; a[1] = h1; a[2] = ldg16(blob, 2); a[3] = ldg16(blob, 3);
 #pragma unroll 1
-        for (int k = 0; k < n64; ++k) {
-            const int nx = k + 1 < n64 ? k + 1 : k;
-            const uint4 b0 = c[4 * nx], b1 = c[4 * nx + 1], b2 = c[4 * nx + 2], b3 = c[4 * nx + 3];
-            s.absorb(lo64(a0)); s.absorb(hi64(a0));
-            s.absorb(lo64(a1)); s.absorb(hi64(a1));
-            s.absorb(lo64(a2)); s.absorb(hi64(a2));
-            s.absorb(lo64(a3)); s.absorb(hi64(a3));
-            a0 = b0; a1 = b1; a2 = b2; a3 = b3;
+    for (uint32_t c = 0; c < n64; c += 2) {
+        if (c + 1 < n64) {
+            b[0] = ldg16(blob, 4 * c + 4); b[1] = ldg16(blob, 4 * c + 5);
+            b[2] = ldg16(blob, 4 * c + 6); b[3] = ldg16(blob, 4 * c + 7);
         }
+        s.absorb(a[0]); s.absorb(a[1]); s.absorb(a[2]); s.absorb(a[3]);
+        if (c + 1 >= n64) break;
+        if (c + 2 < n64) {
+            a[0] = ldg16(blob, 4 * c + 8); a[1] = ldg16(blob, 4 * c + 9);
+            a[2] = ldg16(blob, 4 * c + 10); a[3] = ldg16(blob, 4 * c + 11);
+        }
+        s.absorb(b[0]); s.absorb(b[1]); s.absorb(b[2]); s.absorb(b[3]);
     }
 #pragma unroll 1
-    for (int k = n64 * 4; k < n16; ++k) {
-        const uint4 a = c[k];
-        s.absorb(lo64(a));
-        s.absorb(hi64(a));
-    }
+    for (uint32_t k = n64 * 4u; k < n16; ++k) s.absorb(ldg16(blob, k));
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
-    const uint4 tag = *reinterpret_cast<const uint4*>(blob + kHeader + p.payload);
+    const uint4 tag = ldg16(blob, n16);
     const uint32_t diff = (tag.x ^ (uint32_t)lo) | (tag.y ^ (uint32_t)(lo >> 32)) |
                           (tag.z ^ (uint32_t)hi) | (tag.w ^ (uint32_t)(hi >> 32));
     const uint32_t magic = h0.x & 0xFFFFu, version = (h0.x >> 16) & 0xFFu, flags = h0.x >> 24;
@@ -179,7 +167,7 @@ __device__ int32_t verify_page(const IngressParams& p, int64_t page) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(1024) void ingress_fused_kernel(IngressParams p) {
+__global__ __launch_bounds__(kFusedThreads) void ingress_fused_kernel(IngressParams p) {
     __shared__ int32_t status[64];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
@@ -189,17 +177,19 @@ __global__ __launch_bounds__(1024) void ingress_fused_kernel(IngressParams p) {
         __builtin_amdgcn_s_setprio(3);
         const int32_t st = verify_page(p, page0 + (lane < ppw ? lane : 0));
         status[lane] = st;
-    } else {
+    } else if ((wave & 3) != 0) {  // waves 4 and 8 share the verify wave's SIMD: they idle
         const int items = ppw * p.n_units;
         const int n_batches = (items + 63) / 64;
+        const int dec = wave - 1 - (wave >> 2);
+        const int ndec = nwaves - 1 - ((nwaves - 1) >> 2);
 #pragma unroll 1
-        for (int b = wave - 1; b < n_batches; b += nwaves - 1) {
+        for (int b = dec; b < n_batches; b += ndec) {
             const int item = b * 64 + lane;
             if (item >= items) continue;
             const int u = item / ppw;
             const int64_t page = page0 + (item - u * ppw);
-            const uint4* hq = reinterpret_cast<const uint4*>(ingress_blob(p, page));
-            const uint4 h0 = hq[0], h1 = hq[1];
+            const uint8_t* hq = ingress_blob(p, page);
+            const uint4 h0 = ldg16(hq, 0), h1 = ldg16(hq, 1);
             const uint32_t flags = h0.x >> 24, preset = flags & 0x0Fu, rope_mode = flags >> 4;
             const bool valid = preset >= 1u && preset <= 3u && rope_mode <= 2u &&
                                p.lay_ok[(preset - 1u) * 3u + rope_mode];
@@ -229,11 +219,11 @@ __global__ __launch_bounds__(1024) void ingress_fused_kernel(IngressParams p) {
 #pragma unroll 1
         for (int pl = 0; pl < ppw; ++pl) {
             if (status[pl] == 0) continue;
-            uint4* k = reinterpret_cast<uint4*>(ingress_k(p, page0 + pl));
-            for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) k[i] = make_uint4(0, 0, 0, 0);
-            uint4* v = reinterpret_cast<uint4*>(ingress_v(p, page0 + pl));
+            uint8_t* k = ingress_k(p, page0 + pl);
+            for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) stg16(k, i, make_uint4(0, 0, 0, 0));
+            uint8_t* v = ingress_v(p, page0 + pl);
             if (v)
-                for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) v[i] = make_uint4(0, 0, 0, 0);
+                for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) stg16(v, i, make_uint4(0, 0, 0, 0));
         }
     }
 }
@@ -247,15 +237,16 @@ __global__ void ingress_finalize_kernel(IngressParams p) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t page = i / n16, off = i - page * n16;
-        reinterpret_cast<uint4*>(ingress_k(p, page))[off] = make_uint4(0, 0, 0, 0);
+        stg16(ingress_k(p, page), off, make_uint4(0, 0, 0, 0));
         uint8_t* v = ingress_v(p, page);
-        if (v) reinterpret_cast<uint4*>(v)[off] = make_uint4(0, 0, 0, 0);
+        if (v) stg16(v, off, make_uint4(0, 0, 0, 0));
     }
 }
 
 __global__ void reset_fail_kernel(DeviceState* st) { st->fail = ~0ull; }
 
-hipError_t launch_ingress_fused(const IngressParams& p, int dtype, int waves, hipStream_t s) {
+hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s) {
+    const int waves = kFusedWaves;
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     if (dtype == kHotBf16)
         hipLaunchKernelGGL(ingress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(64 * waves), 0, s, p);

@@ -11,6 +11,13 @@
 
 namespace ztcp {
 
+// Waves per workgroup of the fused kernels: the MAC / verify wave, the waves
+// the dispatcher places on its SIMD (4, 8: they exit at once), and the
+// producers on the other three SIMDs.  12 waves leave each wave 168 VGPRs.
+constexpr int kFusedWaves = 12;
+constexpr int kFusedThreads = 64 * kFusedWaves;
+constexpr int kProducerWaves = kFusedWaves - 1 - (kFusedWaves - 1) / 4;
+
 // Sticky device diagnostics (bit flags, or-ed by kernels).
 constexpr uint32_t kDiagEgressWait = 1u;   // MAC wave's bounded wait expired
 
@@ -19,6 +26,17 @@ struct DeviceState {
     uint32_t diag;             // sticky diagnostic flags
     uint32_t pad;
     unsigned long long fail;   // (page_index << 8) | status of the lowest failing page
+};
+
+// A run of 64-byte chunks the MAC wave absorbs in order: the codes of one
+// section (chunk i belongs to unit unit0 + i / chunks_per_unit and may only be
+// read once that unit's producers have published it) or one section's scales
+// (chunks_per_unit == 0: published with the section's codes).
+struct MacSeg {
+    uint32_t off;              // payload offset
+    uint32_t n;                // 64-byte chunks
+    int32_t unit0;
+    int32_t chunks_per_unit;
 };
 
 struct EgressParams {
@@ -42,6 +60,9 @@ struct EgressParams {
     uint64_t base_seq;
     int32_t ppw;                   // pages per workgroup
     int32_t n_batches;             // ceil(ppw * n_units / 64)
+    MacSeg seg[6];                 // MAC order of the payload (fused path)
+    int32_t n_seg;
+    uint32_t mac_chunks;           // total 64-byte payload chunks
     DeviceState* state;
 };
 
@@ -132,9 +153,26 @@ __device__ __forceinline__ int section_of_unit(const Layout& lay, int u) {
                : 0;
 }
 
+// Byte offset of a section's groups inside a page buffer, walked in (vec,
+// group) row-major order: 32 bytes per group, `skip` extra bytes at the end of
+// each vector (the columns outside the section).
+struct GroupCursor {
+    uint32_t off;
+    int32_t g;
+    __device__ __forceinline__ void step(int32_t gpv, uint32_t skip) {
+        off += 32u;
+        if (++g == gpv) { g = 0; off += skip; }
+    }
+};
+
+__device__ __forceinline__ GroupCursor group_cursor(int32_t G0, int32_t gpv, int32_t col, int32_t head_dim) {
+    const int32_t vec = G0 / gpv, g = G0 - vec * gpv;
+    return GroupCursor{(uint32_t)vec * (uint32_t)head_dim * 2u + (uint32_t)(col + g * 16) * 2u, g};
+}
+
 // Host-side launchers (defined in the .hip translation units).
-hipError_t launch_egress_fused(const EgressParams& p, int dtype, int waves, hipStream_t s);
-hipError_t launch_ingress_fused(const IngressParams& p, int dtype, int waves, hipStream_t s);
+hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s);
+hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s);
 hipError_t launch_egress_generic(const EgressParams& p, int dtype, hipStream_t s);
 hipError_t launch_ingress_generic_impl(const IngressParams& p, int dtype, int32_t* status,
                                        hipStream_t s);
@@ -142,6 +180,7 @@ hipError_t launch_ingress_finalize(const IngressParams& p, hipStream_t s);
 hipError_t launch_reset_fail(DeviceState* st, hipStream_t s);
 hipError_t launch_chacha_xor(const uint8_t* src, uint8_t* dst, size_t len, ChaKey key,
                              uint32_t ctr, uint32_t n0, uint32_t n1, uint32_t n2, hipStream_t s);
+hipError_t launch_selftest(unsigned int* bad, hipStream_t s);
 hipError_t launch_siphash(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
                           uint8_t* tag, hipStream_t s);
 
