@@ -202,6 +202,20 @@ def cpu_baseline(wname: str, budget_s: float) -> dict | None:
     )
 
 
+def calibrate_copy(nbytes: int, reps: int) -> dict:
+    """A plain copy kernel of known size (bitwise_not over int32: reads and writes
+    nbytes each) whose FETCH_SIZE / WRITE_SIZE counters scale the codec's."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    return dict(calibration="bitwise_not int32 copy", bytes_read=nbytes, bytes_written=nbytes, reps=reps)
+
+
 def _traffic(kernel: str, workload: str):
     """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
     f = REPO / "profiles" / "hbm_traffic.json"
@@ -222,7 +236,12 @@ def main() -> None:
     ap.add_argument("--also", default="c2_int4_prefix1g", help="comma list of extra workloads")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run a plain copy kernel of BYTES (counter calibration)")
     a = ap.parse_args()
+    if a.calibrate_copy:
+        print(json.dumps(calibrate_copy(a.calibrate_copy, max(1, a.steps))))
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the cold-page codec has no cross-GPU step "
               "(pages shard independently); run with --gpus 1", file=sys.stderr)

@@ -1,8 +1,8 @@
 """ctypes view of the CPU oracle (oracle/ztcp_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg use this module as the checker.  The product path never
-imports it.
+cpu_baseline leg use this module as the CPU reference the HIP path is
+compared against.  The product path never imports it.
 
 Arrays are numpy; hot pages are passed as raw 16-bit patterns (uint16 views of
 float16 / bfloat16 data).  ``dtype`` is ``FP16`` (the reference's dtype) or

@@ -2,7 +2,7 @@
  * ztcp_oracle.c -- CPU restatement of the ZTCP fused cold-page codec
  * (profile S of research/baseline_codec/csrc/fused_cold_page_cpu.cpp).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP path.  Only tests/,
+ * TEST INFRASTRUCTURE ONLY: the CPU reference the HIP path is compared with.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
  *
  * Build: gcc -O2 -std=c11 -ffp-contract=off (never -ffast-math); the fp32

@@ -1,7 +1,7 @@
 /*
  * ztcp_oracle.h -- CPU restatement of the ZTCP fused cold-page codec.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP path is compared
+ * TEST INFRASTRUCTURE ONLY.  This is the CPU reference the HIP path is compared
  * against (tests/, __graft_entry__.smoke(), and bench.py's cpu_baseline leg).
  * Nothing on the product path links, loads or calls it.
  *
@@ -11,7 +11,7 @@
  * every definition in ztcp_oracle.c cites the reference lines it follows.
  *
  * Hot dtypes: ZO_FP16 is the reference's only dtype (cpp:1499); ZO_BF16 is
- * the extension this build adds (f32 widening of bf16, fp16 scales on the
+ * an extension beyond the reference (f32 widening of bf16, fp16 scales on the
  * wire, bf16 round-to-nearest-even on dequantize).
  */
 #ifndef ZTCP_ORACLE_H

@@ -2,7 +2,7 @@
 
 * registers the ``gpu`` marker (tests that need an MI355X);
 * loads the product package from the ``vlx-tee_amd`` directory as ``vlx_tee_amd``;
-* exposes the CPU oracle (oracle/oracle.py) as the checker.
+* exposes the CPU oracle (oracle/oracle.py) that GPU results are compared with.
 """
 from __future__ import annotations
 

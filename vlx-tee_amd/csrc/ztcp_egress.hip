@@ -8,11 +8,11 @@
 //   * wave 0 (the MAC wave) owns one page per lane.  SipHash is a strictly
 //     sequential chain per page, so 64 pages share one wave's instruction
 //     stream and the kernel can never be shorter than one page's chain
-//     (~290 cycles per 8-byte word on an otherwise idle SIMD).  The MAC wave
+//     (~240 cycles per 8-byte word on an otherwise idle SIMD).  The MAC wave
 //     therefore runs at raised priority on a SIMD of its own: waves 4 and 8,
 //     which the dispatcher places on the same SIMD, exit at once.  It
 //     walks the page in MAC order, reading back ciphertext the producers
-//     wrote (still in L2), one 64-byte chunk ahead of the one it absorbs.
+//     wrote, two 64-byte chunks ahead of the one it absorbs.
 //   * the other 9 waves (producers) take "batches" of 64 (page, unit)
 //     items.  A unit is 32 consecutive groups of one section: its codes
 //     (4 / 8 / 16 keystream blocks) and its 64-byte scale block.  A lane
@@ -175,7 +175,7 @@ struct MacCursor {
     uint32_t i;
 
     __device__ __forceinline__ void fetch(const EgressParams& p, const uint8_t* pay, int ppw,
-                                          const uint32_t* done, uint4 x[4]) {
+                                          const uint32_t* done, uint4 (&x)[4]) {
         const MacSeg s = p.seg[seg];
         if (s.chunks_per_unit && i % (uint32_t)s.chunks_per_unit == 0u) {
             const int32_t u = s.unit0 + (int32_t)(i / (uint32_t)s.chunks_per_unit);
@@ -210,17 +210,7 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, const 
     s.absorb(pg.seq);
     const uint8_t* pay = blob + kHeader;
     MacCursor cur{0, 0};
-    const uint32_t total = p.mac_chunks;
-    uint4 a[4], b[4];
-    cur.fetch(p, pay, ppw, done, a);
-#pragma unroll 1
-    for (uint32_t c = 0; c < total; c += 2) {
-        if (c + 1 < total) cur.fetch(p, pay, ppw, done, b);
-        s.absorb(a[0]); s.absorb(a[1]); s.absorb(a[2]); s.absorb(a[3]);
-        if (c + 1 >= total) break;
-        if (c + 2 < total) cur.fetch(p, pay, ppw, done, a);
-        s.absorb(b[0]); s.absorb(b[1]); s.absorb(b[2]); s.absorb(b[3]);
-    }
+    sip_stream64(s, p.mac_chunks, [&](uint4 (&x)[4]) { cur.fetch(p, pay, ppw, done, x); });
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     if (active)

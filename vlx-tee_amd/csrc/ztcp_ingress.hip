@@ -121,7 +121,7 @@ __device__ void decode_unit(const IngressParams& p, const Layout& lay, int64_t p
 }
 
 // Verdict of one page (cpp:2313-2355); the MAC covers header || payload,
-// read one 64-byte chunk ahead of the chunk being absorbed.
+// read two 64-byte chunks ahead of the chunk being absorbed.
 __device__ int32_t verify_page(const IngressParams& p, int64_t page) {
     const uint8_t* blob = ingress_blob(p, page);
     const uint4 h0 = ldg16(blob, 0), h1 = ldg16(blob, 1);
@@ -130,22 +130,12 @@ __device__ int32_t verify_page(const IngressParams& p, int64_t page) {
     // header || payload = n16 16-byte words (payload % 16 == 0 on this path)
     const uint32_t n16 = (kHeader + p.payload) / 16u;
     const uint32_t n64 = n16 / 4u;
-    uint4 a[4], b[4];
-    a[0] = h0; a[1] = h1; a[2] = ldg16(blob, 2); a[3] = ldg16(blob, 3);
-#pragma unroll 1
-    for (uint32_t c = 0; c < n64; c += 2) {
-        if (c + 1 < n64) {
-            b[0] = ldg16(blob, 4 * c + 4); b[1] = ldg16(blob, 4 * c + 5);
-            b[2] = ldg16(blob, 4 * c + 6); b[3] = ldg16(blob, 4 * c + 7);
-        }
-        s.absorb(a[0]); s.absorb(a[1]); s.absorb(a[2]); s.absorb(a[3]);
-        if (c + 1 >= n64) break;
-        if (c + 2 < n64) {
-            a[0] = ldg16(blob, 4 * c + 8); a[1] = ldg16(blob, 4 * c + 9);
-            a[2] = ldg16(blob, 4 * c + 10); a[3] = ldg16(blob, 4 * c + 11);
-        }
-        s.absorb(b[0]); s.absorb(b[1]); s.absorb(b[2]); s.absorb(b[3]);
-    }
+    uint32_t next = 0;
+    sip_stream64(s, n64, [&](uint4 (&x)[4]) {
+        x[0] = ldg16(blob, next); x[1] = ldg16(blob, next + 1u);
+        x[2] = ldg16(blob, next + 2u); x[3] = ldg16(blob, next + 3u);
+        next += 4u;
+    });
 #pragma unroll 1
     for (uint32_t k = n64 * 4u; k < n16; ++k) s.absorb(ldg16(blob, k));
     uint64_t lo, hi;
