@@ -146,21 +146,9 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
     p.nonce2 = ((uint32_t)aad->layer_id << 16) | (uint32_t)aad->head_group_id;  // cpp:108-109
     p.base_seq = base_seq;
     p.ppw = pages_per_group(batch, ctx->cu_count);
-    p.n_batches = (p.ppw * lay.n_units + 63) / 64;
     p.state = ctx->state;
-    // MAC order of the payload: each section's codes (gated per unit), then its scales
-    p.n_seg = 0;
-    p.mac_chunks = 0;
-    for (int si = 0; si < lay.n_sec; ++si) {
-        const Section& s = lay.sec[si];
-        const uint32_t bpg = (uint32_t)code_bytes_per_group(s.kind);
-        p.seg[p.n_seg++] = MacSeg{s.q_off, (uint32_t)s.n_groups * bpg / 64u, s.unit_begin, (int32_t)(bpg / 2u)};
-        if (s.kind != kSecRaw) p.seg[p.n_seg++] = MacSeg{s.s_off, (uint32_t)s.n_units, s.unit_begin, 0};
-    }
-    for (int i = 0; i < p.n_seg; ++i) p.mac_chunks += p.seg[i].n;
 
     const bool fast = lay.aligned && expected_payload == (int64_t)lay.required && blob_bytes % 16 == 0 &&
-                      p.n_batches <= kMaxBatchFlags &&
                       (descs || (aligned16(k) && aligned16(v) && aligned16(blobs)));
     hipError_t e = fast ? launch_egress_fused(p, g->hot_dtype, stream)
                         : launch_egress_generic(p, g->hot_dtype, stream);

@@ -70,6 +70,44 @@ __device__ __forceinline__ void chacha_block(const ChaKey& key, uint32_t ctr, ui
     ks[14] = x14 + n1;         ks[15] = x15 + n2;
 }
 
+// The same block function split in two, so that a caller can interleave
+// other work (loads, quantization) between the halves of the 10 double rounds.
+struct ChaChaState {
+    uint32_t x[16];
+
+    __device__ __forceinline__ void start(const ChaKey& key, uint32_t ctr, uint32_t n0, uint32_t n1,
+                                          uint32_t n2) {
+        x[0] = 0x61707865u; x[1] = 0x3320646Eu; x[2] = 0x79622D32u; x[3] = 0x6B206574u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[4 + i] = key.w[i];
+        x[12] = ctr; x[13] = n0; x[14] = n1; x[15] = n2;
+    }
+    template <int N>
+    __device__ __forceinline__ void double_rounds() {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            ZTCP_QR(x[0], x[4], x[8], x[12])
+            ZTCP_QR(x[1], x[5], x[9], x[13])
+            ZTCP_QR(x[2], x[6], x[10], x[14])
+            ZTCP_QR(x[3], x[7], x[11], x[15])
+            ZTCP_QR(x[0], x[5], x[10], x[15])
+            ZTCP_QR(x[1], x[6], x[11], x[12])
+            ZTCP_QR(x[2], x[7], x[8], x[13])
+            ZTCP_QR(x[3], x[4], x[9], x[14])
+        }
+    }
+    // Feed-forward (RFC 8439 2.3): ks = rounds(state) + state.
+    __device__ __forceinline__ void finish(const ChaKey& key, uint32_t ctr, uint32_t n0, uint32_t n1,
+                                           uint32_t n2, uint32_t ks[16]) const {
+        ks[0] = x[0] + 0x61707865u;  ks[1] = x[1] + 0x3320646Eu;
+        ks[2] = x[2] + 0x79622D32u;  ks[3] = x[3] + 0x6B206574u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ks[4 + i] = x[4 + i] + key.w[i];
+        ks[12] = x[12] + ctr; ks[13] = x[13] + n0;
+        ks[14] = x[14] + n1;  ks[15] = x[15] + n2;
+    }
+};
+
 // ---------------------------------------------------------------------------
 // SipHash-2-4 with 128-bit output (cpp:401-471).
 // One page per lane; the chain is strictly sequential, so its cost is the

@@ -4,25 +4,32 @@
 // encode_one_cold_page_into_cpu (cpp:1103-1426) driven by
 // fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004).
 //
-// Work decomposition (one workgroup = up to 64 pages, 12 waves):
-//   * wave 0 (the MAC wave) owns one page per lane.  SipHash is a strictly
-//     sequential chain per page, so 64 pages share one wave's instruction
-//     stream and the kernel can never be shorter than one page's chain
-//     (~240 cycles per 8-byte word on an otherwise idle SIMD).  The MAC wave
-//     therefore runs at raised priority on a SIMD of its own: waves 4 and 8,
-//     which the dispatcher places on the same SIMD, exit at once.  It
-//     walks the page in MAC order, reading back ciphertext the producers
-//     wrote, two 64-byte chunks ahead of the one it absorbs.
-//   * the other 9 waves (producers) take "batches" of 64 (page, unit)
-//     items.  A unit is 32 consecutive groups of one section: its codes
-//     (4 / 8 / 16 keystream blocks) and its 64-byte scale block.  A lane
-//     issues the loads of a block's groups, computes the block's keystream
-//     while they are in flight, quantizes, XORs and stores.  Plaintext never
-//     leaves registers.
-//   * a producer publishes a finished batch through a workgroup-scope release
-//     on an LDS flag; the MAC wave acquires the flag before reading a unit.
-//     The MAC wave never blocks producers, and its wait is bounded (a sticky
-//     diagnostic flag records an expired wait and the kernel still ends).
+// Work decomposition (one workgroup = up to 64 pages, 12 waves; lane = page
+// in every wave):
+//   * A "row" is one 64-byte keystream block position of the payload, for all
+//     pages of the workgroup.  Every payload block is exactly one row: a code
+//     row (4 int8 groups, 8 int4 groups or 2 raw groups) or a scale row (the
+//     32 fp16 scales of one unit = 32 groups).  Rows are produced unit by
+//     unit: a unit's code rows, then its scale row.
+//   * Nine producer waves take rows round-robin.  A code row quantizes its
+//     groups (loaded ahead, four at a time, while a keystream is being
+//     computed), stages the scales in LDS, computes the keystream, XORs, and writes the ciphertext into a ring of row slots in
+//     LDS.  From the slot it stores the row to the blobs transposed: four
+//     lanes per page, 64 contiguous bytes per page per store.  A scale row
+//     waits for its unit's code rows, encrypts the staged scales and stores
+//     them the same way.
+//   * Wave 0 runs SipHash for one page per lane, at raised priority on a SIMD
+//     of its own (waves 4 and 8, which the dispatcher places on that SIMD,
+//     exit at once).  It absorbs the header, then the payload in order:
+//     code rows straight from the LDS ring (no global read-back), scale rows
+//     from the blobs once their stores have completed.
+//   * Hand-offs are monotonic LDS counters with workgroup-scope
+//     release/acquire: ring_flag[slot] = code row index + 1 when produced,
+//     mac_used = code rows absorbed (frees ring slots), stage_flag[slot] =
+//     unit + 1 when a scale row is stored (frees its staging slot).  Every
+//     wait is bounded; an expired wait sets a sticky diagnostic bit and the
+//     kernel still ends.  Waits only point backwards in row order, so
+//     progress never depends on a later row.
 // Requires every section to hold a multiple of 32 groups (Layout::aligned),
 // payload == required and 16-byte aligned pointers; otherwise the host routes
 // the call to the generic kernels.
@@ -30,18 +37,127 @@
 
 namespace ztcp {
 
-constexpr uint32_t kSpinLimit = 1u << 22;
+namespace {
 
-__device__ __forceinline__ void wait_flag(const uint32_t* flag, DeviceState* st) {
-    if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u) return;
+constexpr uint32_t kSpinLimit = 1u << 20;  // about 30 ms of s_sleep(1)
+constexpr int kRing = 16;             // code rows between producers and the MAC wave
+constexpr int kStage = 4;             // units whose scales are staged at once
+constexpr int kRowWords = 64 * 16;    // one row: 64 pages x 16 words
+constexpr int kLdsStage = kRing * kRowWords;
+constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
+constexpr int kFlagRing = 0, kFlagStage = kRing, kFlagMacUsed = kRing + kStage;
+constexpr int kLdsBlobs = kLdsFlags + kRing + kStage + 4;  // 64 blob pointers (8-byte aligned)
+constexpr int kLdsWords = kLdsBlobs + 2 * 64;
+static_assert(kLdsBlobs % 2 == 0, "blob table must be 8-byte aligned");
+
+// Word offset of quad q (16 bytes) of page `pg` inside a row slot.  The quad
+// index is XOR-swizzled by page so that lane-per-page accesses and the
+// transposed four-lanes-per-page accesses are both free of bank conflicts.
+__device__ __forceinline__ uint32_t quad_word(int pg, int q) {
+    return (uint32_t)(pg * 16 + ((q ^ ((pg >> 1) & 3)) << 2));
+}
+
+__device__ __forceinline__ uint4 lds_quad(const uint32_t* row, int pg, int q) {
+    return *reinterpret_cast<const uint4*>(row + quad_word(pg, q));
+}
+__device__ __forceinline__ void lds_put_quad(uint32_t* row, int pg, int q, uint4 x) {
+    *reinterpret_cast<uint4*>(row + quad_word(pg, q)) = x;
+}
+
+// Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
+__device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, DeviceState* st) {
+    if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
     for (uint32_t spin = 0;; ++spin) {
-        __builtin_amdgcn_s_sleep(2);
-        if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u) return;
+        __builtin_amdgcn_s_sleep(1);
+        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
         if (spin >= kSpinLimit) {
             atomicOr(&st->diag, kDiagEgressWait);
             return;
         }
     }
+}
+
+__device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
+    __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Row geometry of one section (all values wave-uniform).
+struct SecRows {
+    int32_t kind, nblk, rpu, n_units;
+    int32_t row_begin, code_begin;
+    int32_t qunit_begin;  // units of quantized sections before this one (staging order)
+    int32_t gpv, col, src;
+    uint32_t q_off, s_off;
+};
+
+__device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t row_begin, int32_t code_begin,
+                                            int32_t qunit_begin) {
+    SecRows s;
+    s.kind = ZTCP_SEC_FIELD(lay, si, kind);
+    s.nblk = s.kind == kSecInt8 ? 8 : (s.kind == kSecInt4 ? 4 : 16);
+    s.rpu = s.nblk + (s.kind != kSecRaw ? 1 : 0);
+    s.n_units = ZTCP_SEC_FIELD(lay, si, n_units);
+    s.row_begin = row_begin;
+    s.code_begin = code_begin;
+    s.qunit_begin = qunit_begin;
+    s.gpv = ZTCP_SEC_FIELD(lay, si, gpv);
+    s.col = ZTCP_SEC_FIELD(lay, si, col);
+    s.src = ZTCP_SEC_FIELD(lay, si, src);
+    s.q_off = ZTCP_SEC_FIELD(lay, si, q_off);
+    s.s_off = ZTCP_SEC_FIELD(lay, si, s_off);
+    return s;
+}
+
+struct Row {
+    int32_t valid;
+    int32_t scale;    // 1: scale row
+    int32_t u, j;     // unit in section, code block in unit
+    int32_t g;        // unit index among the page's quantized units (staging slot order)
+    int32_t cidx;     // code row index (scale row: the unit's first code row)
+    int32_t block;    // payload block index (keystream counter - 1)
+    SecRows s;
+};
+
+// Row r of the production order: section by section, unit by unit, a unit's
+// code rows then its scale row.
+__device__ __forceinline__ Row row_info(const Layout& lay, int32_t r) {
+    Row row{};
+    int32_t rb = 0, cb = 0, qb = 0;
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= lay.n_sec || row.valid) continue;
+        const SecRows s = sec_rows(lay, si, rb, cb, qb);
+        const int32_t rows = s.n_units * s.rpu;
+        if (r >= rb && r < rb + rows) {
+            const int32_t local = r - rb;
+            row.valid = 1;
+            // rpu is 9, 5 or 16: constant divisors keep this on the scalar unit
+            row.u = s.kind == kSecInt8 ? local / 9 : (s.kind == kSecInt4 ? local / 5 : local / 16);
+            row.j = local - row.u * s.rpu;
+            row.scale = row.j == s.nblk;
+            row.g = s.qunit_begin + row.u;
+            row.cidx = cb + row.u * s.nblk + (row.scale ? 0 : row.j);
+            row.block = row.scale ? (int32_t)(s.s_off / 64u) + row.u
+                                  : (int32_t)(s.q_off / 64u) + row.u * s.nblk + row.j;
+            row.s = s;
+        }
+        rb += rows;
+        cb += s.n_units * s.nblk;
+        if (s.kind != kSecRaw) qb += s.n_units;
+    }
+    return row;
+}
+
+__device__ __forceinline__ int32_t total_rows(const Layout& lay) {
+    int32_t t = 0;
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= lay.n_sec) continue;
+        const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
+        const int32_t rpu = kind == kSecInt8 ? 9 : (kind == kSecInt4 ? 5 : 16);
+        t += ZTCP_SEC_FIELD(lay, si, n_units) * rpu;
+    }
+    return t;
 }
 
 __device__ __forceinline__ void load_group(const uint8_t* p, uint32_t w[8]) {
@@ -50,151 +166,229 @@ __device__ __forceinline__ void load_group(const uint8_t* p, uint32_t w[8]) {
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
 }
 
-__device__ __forceinline__ void store_block(uint8_t* dst, const uint32_t pt[16], const uint32_t ks[16]) {
+// Issues the hot loads of half h of a code row: groups [4h, 4h + 4) of the
+// row's 4 (int8), 8 (int4) or 2 (raw) groups.
+__device__ __forceinline__ void load_half(const EgressParams& p, const EgressPage& pg, const Row& row, int h,
+                                          uint32_t (&w)[4][8]) {
+    const int ng = row.s.kind == kSecInt8 ? 4 : (row.s.kind == kSecInt4 ? 8 : 2);
+    const uint8_t* src = row.s.src ? pg.v : pg.k;
+    GroupCursor cur = group_cursor(row.u * 32 + row.j * ng + 4 * h, row.s.gpv, row.s.col, p.head_dim);
+    const uint32_t skip = (uint32_t)(p.head_dim - row.s.gpv * 16) * 2u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        stg16(dst, i, make_uint4(pt[4 * i] ^ ks[4 * i], pt[4 * i + 1] ^ ks[4 * i + 1],
-                                 pt[4 * i + 2] ^ ks[4 * i + 2], pt[4 * i + 3] ^ ks[4 * i + 3]));
+    for (int i = 0; i < 4; ++i) {
+        if (i < ng) {
+            load_group(src + cur.off, w[i]);
+            cur.step(row.s.gpv, skip);
+        }
+    }
 }
 
-// One unit of a quantized section.  GPB = groups per 64-byte code block
-// (4 for int8, 8 for int4).  Per block: quantize the groups loaded during the
-// previous block's keystream, issue the next block's loads, compute this
-// block's keystream, XOR and store.  The unit's 32 scales are staged in this
-// lane's LDS slot (word-major, so lanes hit distinct banks) and encrypted as
-// the unit's scale block at the end.
+// Stores one row slot to the blobs: lane l writes quad (l & 3) of page
+// 16 k + (l >> 2), so each store instruction writes 64 contiguous bytes of 16
+// pages.  tb[k] is that page's blob pointer (null past the last page).
+__device__ __forceinline__ void store_row(const uint32_t* slot, uint8_t* const (&tb)[4], uint32_t blob_off,
+                                          int lane) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int pr = 16 * k + (lane >> 2), q = lane & 3;
+        const uint4 x = lds_quad(slot, pr, q);
+        if (tb[k]) stg16(tb[k] + blob_off, q, x);
+    }
+}
+
+struct ProducerCtx {
+    const EgressParams* p;
+    EgressPage pg;
+    uint32_t n0, n1, n2;
+    uint32_t* lds;
+    uint8_t* tb[4];
+    int lane;
+};
+
+// Quantizes groups w[0..3] (int8: 4 code words each, int4: 2) into pt[] and
+// their fp16 scales into sc[] (two per word, low half first).
+template <int DT, int BITS>
+__device__ __forceinline__ void quant_half(const uint32_t (&w)[4][8], uint32_t* pt, uint32_t* sc) {
+    constexpr int CW = BITS == 8 ? 4 : 2;
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+        uint32_t qa[4], qb[4];
+        const uint32_t sa = quant_group<DT, BITS>(w[i], qa);
+        const uint32_t sbb = quant_group<DT, BITS>(w[i + 1], qb);
+#pragma unroll
+        for (int t = 0; t < CW; ++t) {
+            pt[CW * i + t] = qa[t];
+            pt[CW * (i + 1) + t] = qb[t];
+        }
+        sc[i / 2] = sa | (sbb << 16);
+    }
+}
+
+// One code row.  w holds the row's first four groups (loaded a row ahead);
+// an int4 row loads its second four during the first half of the keystream.
+// The next row's first groups are loaded as soon as w is free.
 template <int DT, int KIND>
-__device__ __forceinline__ void produce_quant_unit(const EgressParams& p, const uint8_t* src,
-                                                   uint8_t* pay, int32_t lu, int32_t gpv,
-                                                   int32_t col, uint32_t q_off, uint32_t s_off,
-                                                   uint32_t n0, uint32_t n1, uint32_t n2,
-                                                   uint32_t* slot) {
-    constexpr int GPB = KIND == kSecInt8 ? 4 : 8;
-    constexpr int NBLK = 32 / GPB;
-    constexpr int CW = KIND == kSecInt8 ? 4 : 2;  // code words per group
-    const int32_t G0 = lu * 32;
-    GroupCursor cur = group_cursor(G0, gpv, col, p.head_dim);
-    const uint32_t skip = (uint32_t)(p.head_dim - gpv * 16) * 2u;
-    const uint32_t blk0 = 1u + (q_off + (uint32_t)G0 * (uint32_t)(CW * 4)) / 64u;
-    uint8_t* code = pay + q_off + (uint32_t)(G0 * CW * 4);
-    uint32_t w[GPB][8];
+__device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt, bool prefetch,
+                                         uint32_t (&w)[4][8]) {
+    constexpr int SW = KIND == kSecInt8 ? 2 : (KIND == kSecInt4 ? 4 : 0);  // scale words per row
+    const EgressParams& p = *c.p;
+    uint32_t* flags = c.lds + kLdsFlags;
+    uint32_t pt[16];
+    uint32_t sc[4];
+    ChaChaState st;
+    st.start(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2);
+    if constexpr (KIND == kSecRaw) {
 #pragma unroll
-    for (int i = 0; i < GPB; ++i) {
-        load_group(src + cur.off, w[i]);
-        cur.step(gpv, skip);
-    }
-#pragma unroll 1
-    for (int j = 0; j < NBLK; ++j) {
-        uint32_t pt[16];
-#pragma unroll
-        for (int i = 0; i < GPB; i += 2) {
-            uint32_t qa[4], qb[4];
-            const uint32_t sa = quant_group<DT, KIND == kSecInt8 ? 8 : 4>(w[i], qa);
-            const uint32_t sbb = quant_group<DT, KIND == kSecInt8 ? 8 : 4>(w[i + 1], qb);
-#pragma unroll
-            for (int t = 0; t < CW; ++t) {
-                pt[CW * i + t] = qa[t];
-                pt[CW * (i + 1) + t] = qb[t];
-            }
-            slot[(j * (GPB / 2) + i / 2) * 64] = sa | (sbb << 16);
+        for (int t = 0; t < 8; ++t) {
+            pt[t] = w[0][t];
+            pt[8 + t] = w[1][t];
         }
-        if (j + 1 < NBLK) {
-#pragma unroll
-            for (int i = 0; i < GPB; ++i) {
-                load_group(src + cur.off, w[i]);
-                cur.step(gpv, skip);
-            }
-        }
-        uint32_t ks[16];
-        chacha_block(p.key, blk0 + (uint32_t)j, n0, n1, n2, ks);
-        store_block(code + (uint32_t)j * 64u, pt, ks);
+        if (prefetch) load_half(p, c.pg, nxt, 0, w);
+        st.double_rounds<10>();
+    } else if constexpr (KIND == kSecInt8) {
+        quant_half<DT, 8>(w, pt, sc);
+        if (prefetch) load_half(p, c.pg, nxt, 0, w);
+        st.double_rounds<10>();
+    } else {
+        quant_half<DT, 4>(w, pt, sc);
+        load_half(p, c.pg, row, 1, w);
+        st.double_rounds<5>();
+        quant_half<DT, 4>(w, pt + 8, sc + 2);
+        if (prefetch) load_half(p, c.pg, nxt, 0, w);
+        st.double_rounds<5>();
     }
-    uint32_t sc[16];
+    if constexpr (SW > 0) {
+        // the unit's staging slot is free once unit g - kStage's scale row is done
+        uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
+        wait_ge(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
 #pragma unroll
-    for (int t = 0; t < 16; ++t) sc[t] = slot[t * 64];
-    const uint32_t s_unit = s_off + (uint32_t)lu * 64u;
+        for (int t = 0; t < SW; ++t) {
+            const int wd = row.j * SW + t;  // logical scale word of this lane's page
+            stage[quad_word(c.lane, wd >> 2) + (wd & 3)] = sc[t];
+        }
+    }
     uint32_t ks[16];
-    chacha_block(p.key, 1u + s_unit / 64u, n0, n1, n2, ks);
-    store_block(pay + s_unit, sc, ks);
+    st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
+    uint32_t* slot = c.lds + (row.cidx % kRing) * kRowWords;
+    wait_ge(&flags[kFlagMacUsed], row.cidx - kRing + 1, p.state);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        lds_put_quad(slot, c.lane, q,
+                     make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
+                                pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
+    store_row(slot, c.tb, (uint32_t)kHeader + 64u * (uint32_t)row.block, c.lane);
+    publish(&flags[kFlagRing + row.cidx % kRing], (uint32_t)row.cidx + 1u);
 }
 
-// One unit of a raw (PRESERVE_RAW) section: 32 groups of hot bytes.
-__device__ __forceinline__ void produce_raw_unit(const EgressParams& p, const uint8_t* src,
-                                                 uint8_t* pay, int32_t lu, int32_t gpv,
-                                                 int32_t col, uint32_t q_off, uint32_t n0,
-                                                 uint32_t n1, uint32_t n2) {
-    const int32_t G0 = lu * 32;
-    GroupCursor cur = group_cursor(G0, gpv, col, p.head_dim);
-    const uint32_t skip = (uint32_t)(p.head_dim - gpv * 16) * 2u;
-    const uint32_t blk0 = 1u + (q_off + (uint32_t)G0 * 32u) / 64u;
-    uint32_t pt[16];
-    load_group(src + cur.off, pt);
-    cur.step(gpv, skip);
-    load_group(src + cur.off, pt + 8);
-    cur.step(gpv, skip);
+__device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row, const Row& nxt, bool prefetch,
+                                          uint32_t (&w)[4][8]) {
+    const EgressParams& p = *c.p;
+    uint32_t* flags = c.lds + kLdsFlags;
+    if (prefetch) load_half(p, c.pg, nxt, 0, w);
+    uint32_t ks[16];
+    chacha_block(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
+    // every code row of the unit has staged its scales
 #pragma unroll 1
-    for (int j = 0; j < 16; ++j) {
-        uint32_t ks[16];
-        chacha_block(p.key, blk0 + (uint32_t)j, n0, n1, n2, ks);
-        store_block(pay + q_off + (uint32_t)G0 * 32u + (uint32_t)j * 64u, pt, ks);
-        if (j + 1 < 16) {
-            load_group(src + cur.off, pt);
-            cur.step(gpv, skip);
-            load_group(src + cur.off, pt + 8);
-            cur.step(gpv, skip);
-        }
+    for (int t = 0; t < row.s.nblk; ++t) {
+        const int32_t ci = row.cidx + t;
+        wait_ge(&flags[kFlagRing + ci % kRing], ci + 1, p.state);
     }
+    uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 s = lds_quad(stage, c.lane, q);
+        lds_put_quad(stage, c.lane, q,
+                     make_uint4(s.x ^ ks[4 * q], s.y ^ ks[4 * q + 1], s.z ^ ks[4 * q + 2], s.w ^ ks[4 * q + 3]));
+    }
+    store_row(stage, c.tb, (uint32_t)kHeader + 64u * (uint32_t)row.block, c.lane);
+    // the MAC wave reads scale rows from the blobs: the stores must be complete
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
 }
 
 template <int DT>
-__device__ void produce_unit(const EgressParams& p, int64_t page, int32_t u, uint32_t* slot) {
-    const int si = section_of_unit(p.lay, u);
-    const int32_t kind = ZTCP_SEC_FIELD(p.lay, si, kind);
-    const int32_t srcsel = ZTCP_SEC_FIELD(p.lay, si, src);
-    const int32_t col = ZTCP_SEC_FIELD(p.lay, si, col);
-    const int32_t gpv = ZTCP_SEC_FIELD(p.lay, si, gpv);
-    const int32_t lu = u - ZTCP_SEC_FIELD(p.lay, si, unit_begin);
-    const uint32_t q_off = ZTCP_SEC_FIELD(p.lay, si, q_off);
-    const uint32_t s_off = ZTCP_SEC_FIELD(p.lay, si, s_off);
-    const EgressPage pg = egress_page(p, page);
-    const uint8_t* src = srcsel ? pg.v : pg.k;
-    uint8_t* pay = pg.blob + kHeader;
-    const uint32_t n0 = (uint32_t)pg.seq, n1 = (uint32_t)(pg.seq >> 32);
-    if (kind == kSecInt8)
-        produce_quant_unit<DT, kSecInt8>(p, src, pay, lu, gpv, col, q_off, s_off, n0, n1, pg.nonce2, slot);
-    else if (kind == kSecInt4)
-        produce_quant_unit<DT, kSecInt4>(p, src, pay, lu, gpv, col, q_off, s_off, n0, n1, pg.nonce2, slot);
-    else
-        produce_raw_unit(p, src, pay, lu, gpv, col, q_off, n0, n1, pg.nonce2);
+__device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, int prod, uint32_t* lds) {
+    ProducerCtx c;
+    c.p = &p;
+    c.lane = threadIdx.x & 63;
+    c.pg = egress_page(p, page0 + (c.lane < ppw ? c.lane : 0));
+    c.n0 = (uint32_t)c.pg.seq;
+    c.n1 = (uint32_t)(c.pg.seq >> 32);
+    c.n2 = c.pg.nonce2;
+    c.lds = lds;
+    const uint64_t* blobs = reinterpret_cast<const uint64_t*>(lds + kLdsBlobs);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int pr = 16 * k + (c.lane >> 2);
+        c.tb[k] = pr < ppw ? reinterpret_cast<uint8_t*>(blobs[pr]) : nullptr;
+    }
+    const int32_t total = total_rows(p.lay);
+    uint32_t w[4][8];
+    Row cur = row_info(p.lay, prod);
+    if (cur.valid && !cur.scale) load_half(p, c.pg, cur, 0, w);
+#pragma unroll 1
+    for (int32_t r = prod; r < total; r += kProducerWaves) {
+        const Row nxt = row_info(p.lay, r + kProducerWaves);
+        const bool prefetch = nxt.valid && !nxt.scale;
+        if (cur.scale)
+            scale_row(c, cur, nxt, prefetch, w);
+        else if (cur.s.kind == kSecInt8)
+            code_row<DT, kSecInt8>(c, cur, nxt, prefetch, w);
+        else if (cur.s.kind == kSecInt4)
+            code_row<DT, kSecInt4>(c, cur, nxt, prefetch, w);
+        else
+            code_row<DT, kSecRaw>(c, cur, nxt, prefetch, w);
+        cur = nxt;
+    }
 }
 
-// Walks the payload's 64-byte chunks in MAC order, waiting for each unit's
-// batch flags before its first chunk is read.
-struct MacCursor {
-    int32_t seg;
-    uint32_t i;
+// The MAC wave's view of the payload: each section's code rows (LDS ring),
+// then its scale rows (blobs).
+struct MacFeed {
+    int32_t si, phase, i;
+    int32_t cidx;
+    int32_t row_begin, code_begin, qunit_begin;
 
-    __device__ __forceinline__ void fetch(const EgressParams& p, const uint8_t* pay, int ppw,
-                                          const uint32_t* done, uint4 (&x)[4]) {
-        const MacSeg s = p.seg[seg];
-        if (s.chunks_per_unit && i % (uint32_t)s.chunks_per_unit == 0u) {
-            const int32_t u = s.unit0 + (int32_t)(i / (uint32_t)s.chunks_per_unit);
-            const int32_t b0 = (u * ppw) / 64, b1 = (u * ppw + ppw - 1) / 64;
-            wait_flag(&done[b0], p.state);
-            if (b1 != b0) wait_flag(&done[b1], p.state);
+    __device__ __forceinline__ void fetch(const EgressParams& p, const uint8_t* pay, const uint32_t* lds,
+                                          int lane, uint4 (&x)[4], int32_t& tag) {
+        const uint32_t* flags = lds + kLdsFlags;
+        const SecRows s = sec_rows(p.lay, si, row_begin, code_begin, qunit_begin);
+        if (phase == 0) {
+            const uint32_t* slot = lds + (cidx % kRing) * kRowWords;
+            wait_ge(&flags[kFlagRing + cidx % kRing], cidx + 1, p.state);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[q] = lds_quad(slot, lane, q);
+            tag = cidx + 1;
+            ++cidx;
+            if (++i == s.n_units * s.nblk) {
+                i = 0;
+                phase = s.kind != kSecRaw ? 1 : 2;
+            }
+        } else {
+            const int32_t g = s.qunit_begin + i;
+            wait_ge(&flags[kFlagStage + g % kStage], g + 1, p.state);
+            const uint8_t* q = pay + s.s_off + 64u * (uint32_t)i;
+            x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
+            tag = 0;
+            if (++i == s.n_units) phase = 2;
         }
-        const uint8_t* q = pay + s.off + 64u * i;
-        x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
-        if (++i == s.n) { ++seg; i = 0; }
+        if (phase == 2) {  // next section
+            row_begin += s.n_units * s.rpu;
+            code_begin += s.n_units * s.nblk;
+            if (s.kind != kSecRaw) qunit_begin += s.n_units;
+            ++si;
+            phase = 0;
+            i = 0;
+        }
     }
 };
 
 template <int DT>
-__device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, const uint32_t* done) {
+__device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
     const int lane = threadIdx.x & 63;
     const bool active = lane < ppw;
-    const int64_t page = page0 + (active ? lane : 0);
-    const EgressPage pg = egress_page(p, page);
+    const EgressPage pg = egress_page(p, page0 + (active ? lane : 0));
     uint8_t* blob = pg.blob;
     if (active) {  // header (cpp:1129-1140)
         stg16(blob, 0, make_uint4((uint32_t)p.hdr0, (uint32_t)(p.hdr0 >> 32), (uint32_t)pg.hdr1,
@@ -204,13 +398,32 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, const 
     }
     Sip s;
     s.init(p.mk0, p.mk1);
-    s.absorb(p.hdr0);
-    s.absorb(pg.hdr1);
-    s.absorb(pg.token);
-    s.absorb(pg.seq);
+    const uint64_t hdr[4] = {p.hdr0, pg.hdr1, pg.token, pg.seq};
+    s.absorb_words<4>(hdr);
     const uint8_t* pay = blob + kHeader;
-    MacCursor cur{0, 0};
-    sip_stream64(s, p.mac_chunks, [&](uint4 (&x)[4]) { cur.fetch(p, pay, ppw, done, x); });
+    uint32_t* used = lds + kLdsFlags + kFlagMacUsed;
+    MacFeed feed{0, 0, 0, 0, 0, 0, 0};
+    const int32_t total = total_rows(p.lay);
+    // three chunks in flight: two fetched ahead of the one being absorbed; a
+    // code row's ring slot is released once it has been absorbed
+    uint4 x0[4], x1[4], x2[4];
+    int32_t t0 = 0, t1 = 0, t2 = 0;
+    if (total > 0) feed.fetch(p, pay, lds, lane, x0, t0);
+    if (total > 1) feed.fetch(p, pay, lds, lane, x1, t1);
+#pragma unroll 1
+    for (int32_t c = 0; c < total; c += 3) {
+        if (c + 2 < total) feed.fetch(p, pay, lds, lane, x2, t2);
+        s.absorb64(x0);
+        if (t0) publish(used, (uint32_t)t0);
+        if (c + 1 >= total) break;
+        if (c + 3 < total) feed.fetch(p, pay, lds, lane, x0, t0);
+        s.absorb64(x1);
+        if (t1) publish(used, (uint32_t)t1);
+        if (c + 2 >= total) break;
+        if (c + 4 < total) feed.fetch(p, pay, lds, lane, x1, t1);
+        s.absorb64(x2);
+        if (t2) publish(used, (uint32_t)t2);
+    }
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     if (active)
@@ -218,53 +431,41 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, const 
               make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)));
 }
 
-// Dynamic LDS: scale staging for the producer waves (16 words x 64 lanes
-// each), then one completion flag per batch.
-constexpr int kStageWords = kProducerWaves * 16 * 64;
-
 template <int DT>
 __global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParams p) {
-    extern __shared__ uint32_t lds[];
-    uint32_t* done = lds + kStageWords;
+    extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
-    const int items = ppw * p.lay.n_units;
-    const int n_batches = (items + 63) / 64;
-    for (int i = threadIdx.x; i < n_batches; i += blockDim.x) done[i] = 0u;
+    for (int i = threadIdx.x; i < kRing + kStage + 4; i += blockDim.x) lds[kLdsFlags + i] = 0u;
+    if (threadIdx.x < 64) {
+        uint64_t* blobs = reinterpret_cast<uint64_t*>(lds + kLdsBlobs);
+        const int pg = (int)threadIdx.x < ppw ? (int)threadIdx.x : 0;
+        blobs[threadIdx.x] = reinterpret_cast<uint64_t>(egress_page(p, page0 + pg).blob);
+    }
     __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nwaves = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6;
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
-        egress_mac<DT>(p, page0, ppw, done);
+        egress_mac<DT>(p, page0, ppw, lds);
         return;
     }
     if ((wave & 3) == 0) return;  // leave the MAC wave's SIMD to it
     const int prod = wave - 1 - (wave >> 2);
-    const int nprod = nwaves - 1 - ((nwaves - 1) >> 2);
     if (prod >= kProducerWaves) return;  // never: launched with kFusedWaves waves
-    uint32_t* slot = lds + prod * 16 * 64 + lane;
-#pragma unroll 1
-    for (int b = prod; b < n_batches; b += nprod) {
-        const int item = b * 64 + lane;
-        if (item < items) {
-            const int u = item / ppw;
-            produce_unit<DT>(p, page0 + (item - u * ppw), u, slot);
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // every store of this batch has completed
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (lane == 0) __hip_atomic_store(&done[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
+    egress_produce<DT>(p, page0, ppw, prod, lds);
 }
 
+}  // namespace
+
+size_t egress_fused_lds_bytes() { return (size_t)kLdsWords * sizeof(uint32_t); }
+
 hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) {
-    const int waves = kFusedWaves;
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
-    const size_t lds = ((size_t)kStageWords + (size_t)p.n_batches) * sizeof(uint32_t);
+    const size_t lds = egress_fused_lds_bytes();  // above 64 KiB: gfx950 has 160 KiB per CU
     if (dtype == kHotBf16)
-        hipLaunchKernelGGL(egress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(64 * waves), lds, s, p);
+        hipLaunchKernelGGL(egress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kFusedThreads), lds, s, p);
     else
-        hipLaunchKernelGGL(egress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(64 * waves), lds, s, p);
+        hipLaunchKernelGGL(egress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kFusedThreads), lds, s, p);
     return hipGetLastError();
 }
 

@@ -28,17 +28,6 @@ struct DeviceState {
     unsigned long long fail;   // (page_index << 8) | status of the lowest failing page
 };
 
-// A run of 64-byte chunks the MAC wave absorbs in order: the codes of one
-// section (chunk i belongs to unit unit0 + i / chunks_per_unit and may only be
-// read once that unit's producers have published it) or one section's scales
-// (chunks_per_unit == 0: published with the section's codes).
-struct MacSeg {
-    uint32_t off;              // payload offset
-    uint32_t n;                // 64-byte chunks
-    int32_t unit0;
-    int32_t chunks_per_unit;
-};
-
 struct EgressParams {
     const uint8_t* k;              // contiguous K pages (hot elements, 2 bytes each)
     const uint8_t* v;              // contiguous V pages or nullptr
@@ -59,10 +48,6 @@ struct EgressParams {
     uint32_t nonce2;               // (layer_id << 16) | head_group_id
     uint64_t base_seq;
     int32_t ppw;                   // pages per workgroup
-    int32_t n_batches;             // ceil(ppw * n_units / 64)
-    MacSeg seg[6];                 // MAC order of the payload (fused path)
-    int32_t n_seg;
-    uint32_t mac_chunks;           // total 64-byte payload chunks
     DeviceState* state;
 };
 
