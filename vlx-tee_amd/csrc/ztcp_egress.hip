@@ -11,12 +11,14 @@
 //     row (4 int8 groups, 8 int4 groups or 2 raw groups) or a scale row (the
 //     32 fp16 scales of one unit = 32 groups).  Rows are produced unit by
 //     unit: a unit's code rows, then its scale row.
-//   * Nine producer waves take rows round-robin.  A code row quantizes its
-//     groups (loaded ahead, four at a time, while a keystream is being
-//     computed), stages the scales in LDS, computes the keystream, XORs, and writes the ciphertext into a ring of row slots in
+//   * Nine producer waves take code rows in order from an LDS counter.  A
+//     code row quantizes its groups (loaded ahead, four at a time, while a
+//     keystream is being computed), stages the scales in LDS, computes the
+//     keystream, XORs, and writes the ciphertext into a ring of row slots in
 //     LDS.  From the slot it stores the row to the blobs transposed: four
-//     lanes per page, 64 contiguous bytes per page per store.  A scale row
-//     waits for its unit's code rows, encrypts the staged scales and stores
+//     lanes per page, 64 contiguous bytes per page per store.  The wave that
+//     stages a unit's last scales (an LDS counter per staging slot) also
+//     makes the unit's scale row: it encrypts the staged scales and stores
 //     them the same way.
 //   * Wave 0 runs SipHash for one page per lane, at raised priority on a SIMD
 //     of its own (waves 4 and 8, which the dispatcher places on that SIMD,
@@ -26,7 +28,8 @@
 //   * Hand-offs are monotonic LDS counters with workgroup-scope
 //     release/acquire: ring_flag[slot] = code row index + 1 when produced,
 //     mac_used = code rows absorbed (frees ring slots), stage_flag[slot] =
-//     unit + 1 when a scale row is stored (frees its staging slot).  Every
+//     unit + 1 when a scale row has read its staging slot, scale_flag[slot] =
+//     unit + 1 once the scale row's stores have completed.  Every
 //     wait is bounded; an expired wait sets a sticky diagnostic bit and the
 //     kernel still ends.  Waits only point backwards in row order, so
 //     progress never depends on a later row.
@@ -40,13 +43,20 @@ namespace ztcp {
 namespace {
 
 constexpr uint32_t kSpinLimit = 1u << 20;  // about 30 ms of s_sleep(1)
-constexpr int kRing = 16;             // code rows between producers and the MAC wave
-constexpr int kStage = 4;             // units whose scales are staged at once
+constexpr int kRing = 24;             // code rows between producers and the MAC wave
+constexpr int kStage = 8;             // units whose scales are staged at once
 constexpr int kRowWords = 64 * 16;    // one row: 64 pages x 16 words
 constexpr int kLdsStage = kRing * kRowWords;
+constexpr int kScaleSlots = 64;      // scale rows the MAC wave may still be waiting for
 constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
-constexpr int kFlagRing = 0, kFlagStage = kRing, kFlagMacUsed = kRing + kStage;
-constexpr int kLdsBlobs = kLdsFlags + kRing + kStage + 4;  // 64 blob pointers (8-byte aligned)
+constexpr int kFlagRing = 0;                          // [kRing] code row index + 1
+constexpr int kFlagStage = kFlagRing + kRing;         // [kStage] unit + 1: staging slot free
+constexpr int kFlagCount = kFlagStage + kStage;       // [kStage] code rows staged in the slot
+constexpr int kFlagScale = kFlagCount + kStage;       // [kScaleSlots] unit + 1: scale row stored
+constexpr int kFlagMacUsed = kFlagScale + kScaleSlots;  // code rows absorbed by the MAC wave
+constexpr int kFlagTask = kFlagMacUsed + 1;           // next code row to hand out
+constexpr int kNumFlags = kFlagMacUsed + 4;
+constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byte aligned)
 constexpr int kLdsWords = kLdsBlobs + 2 * 64;
 static_assert(kLdsBlobs % 2 == 0, "blob table must be 8-byte aligned");
 
@@ -84,20 +94,18 @@ __device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
 // Row geometry of one section (all values wave-uniform).
 struct SecRows {
     int32_t kind, nblk, rpu, n_units;
-    int32_t row_begin, code_begin;
+    int32_t code_begin;
     int32_t qunit_begin;  // units of quantized sections before this one (staging order)
     int32_t gpv, col, src;
     uint32_t q_off, s_off;
 };
 
-__device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t row_begin, int32_t code_begin,
-                                            int32_t qunit_begin) {
+__device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t code_begin, int32_t qunit_begin) {
     SecRows s;
     s.kind = ZTCP_SEC_FIELD(lay, si, kind);
     s.nblk = s.kind == kSecInt8 ? 8 : (s.kind == kSecInt4 ? 4 : 16);
     s.rpu = s.nblk + (s.kind != kSecRaw ? 1 : 0);
     s.n_units = ZTCP_SEC_FIELD(lay, si, n_units);
-    s.row_begin = row_begin;
     s.code_begin = code_begin;
     s.qunit_begin = qunit_begin;
     s.gpv = ZTCP_SEC_FIELD(lay, si, gpv);
@@ -110,42 +118,51 @@ __device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t r
 
 struct Row {
     int32_t valid;
-    int32_t scale;    // 1: scale row
+    int32_t scale;    // 1: last code row of its unit (quantized sections)
     int32_t u, j;     // unit in section, code block in unit
     int32_t g;        // unit index among the page's quantized units (staging slot order)
-    int32_t cidx;     // code row index (scale row: the unit's first code row)
+    int32_t cidx;     // code row index = production order
     int32_t block;    // payload block index (keystream counter - 1)
     SecRows s;
 };
 
-// Row r of the production order: section by section, unit by unit, a unit's
-// code rows then its scale row.
-__device__ __forceinline__ Row row_info(const Layout& lay, int32_t r) {
+// Code row t: the payload's code blocks in order, which is also the order of
+// production.  A unit's scale row is produced right after its last code row,
+// by the same wave.
+__device__ __forceinline__ Row row_info(const Layout& lay, int32_t t) {
     Row row{};
-    int32_t rb = 0, cb = 0, qb = 0;
+    int32_t cb = 0, qb = 0;
 #pragma unroll
     for (int si = 0; si < 3; ++si) {
         if (si >= lay.n_sec || row.valid) continue;
-        const SecRows s = sec_rows(lay, si, rb, cb, qb);
-        const int32_t rows = s.n_units * s.rpu;
-        if (r >= rb && r < rb + rows) {
-            const int32_t local = r - rb;
+        const SecRows s = sec_rows(lay, si, cb, qb);
+        const int32_t n = s.n_units * s.nblk;
+        if (t >= cb && t < cb + n) {
+            const int32_t local = t - cb;
             row.valid = 1;
-            // rpu is 9, 5 or 16: constant divisors keep this on the scalar unit
-            row.u = s.kind == kSecInt8 ? local / 9 : (s.kind == kSecInt4 ? local / 5 : local / 16);
-            row.j = local - row.u * s.rpu;
-            row.scale = row.j == s.nblk;
+            row.u = local / s.nblk;  // nblk is 8, 4 or 16
+            row.j = local - row.u * s.nblk;
+            row.scale = s.kind != kSecRaw && row.j == s.nblk - 1;
             row.g = s.qunit_begin + row.u;
-            row.cidx = cb + row.u * s.nblk + (row.scale ? 0 : row.j);
-            row.block = row.scale ? (int32_t)(s.s_off / 64u) + row.u
-                                  : (int32_t)(s.q_off / 64u) + row.u * s.nblk + row.j;
+            row.cidx = t;
+            row.block = (int32_t)(s.q_off / 64u) + local;
             row.s = s;
         }
-        rb += rows;
-        cb += s.n_units * s.nblk;
+        cb += n;
         if (s.kind != kSecRaw) qb += s.n_units;
     }
     return row;
+}
+
+__device__ __forceinline__ int32_t total_code_rows(const Layout& lay) {
+    int32_t t = 0;
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= lay.n_sec) continue;
+        const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
+        t += ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16));
+    }
+    return t;
 }
 
 __device__ __forceinline__ int32_t total_rows(const Layout& lay) {
@@ -280,19 +297,16 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     publish(&flags[kFlagRing + row.cidx % kRing], (uint32_t)row.cidx + 1u);
 }
 
-__device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row, const Row& nxt, bool prefetch,
-                                          uint32_t (&w)[4][8]) {
+// The scale row of row.u's unit, run by the wave that staged the unit's last
+// scales: encrypts the staged scales in place and stores the block.  Frees
+// the staging slot at once; the stores' completion is published later
+// (publish_scale) so that the wave does not wait for them here.
+__device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) {
     const EgressParams& p = *c.p;
     uint32_t* flags = c.lds + kLdsFlags;
-    if (prefetch) load_half(p, c.pg, nxt, 0, w);
+    const uint32_t block = row.s.s_off / 64u + (uint32_t)row.u;
     uint32_t ks[16];
-    chacha_block(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
-    // every code row of the unit has staged its scales
-#pragma unroll 1
-    for (int t = 0; t < row.s.nblk; ++t) {
-        const int32_t ci = row.cidx + t;
-        wait_ge(&flags[kFlagRing + ci % kRing], ci + 1, p.state);
-    }
+    chacha_block(p.key, 1u + block, c.n0, c.n1, c.n2, ks);
     uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -300,15 +314,20 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row, 
         lds_put_quad(stage, c.lane, q,
                      make_uint4(s.x ^ ks[4 * q], s.y ^ ks[4 * q + 1], s.z ^ ks[4 * q + 2], s.w ^ ks[4 * q + 3]));
     }
-    store_row(stage, c.tb, (uint32_t)kHeader + 64u * (uint32_t)row.block, c.lane);
-    // the MAC wave reads scale rows from the blobs: the stores must be complete
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    store_row(stage, c.tb, (uint32_t)kHeader + 64u * block, c.lane);
+    flags[kFlagCount + row.g % kStage] = 0u;
     publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
 }
 
+// Publishes that scale row g is in the blobs, for the MAC wave to read.
+__device__ __forceinline__ void publish_scale(uint32_t* flags, int32_t g) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    publish(&flags[kFlagScale + g % kScaleSlots], (uint32_t)g + 1u);
+}
+
 template <int DT>
-__device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, int prod, uint32_t* lds) {
+__device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
     ProducerCtx c;
     c.p = &p;
     c.lane = threadIdx.x & 63;
@@ -323,24 +342,53 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, in
         const int pr = 16 * k + (c.lane >> 2);
         c.tb[k] = pr < ppw ? reinterpret_cast<uint8_t*>(blobs[pr]) : nullptr;
     }
-    const int32_t total = total_rows(p.lay);
+    const int32_t total = total_code_rows(p.lay);
+    uint32_t* flags = lds + kLdsFlags;
+    // code rows are handed out in order from an LDS counter, one row ahead of
+    // the one being made (so its groups can be prefetched): a slower wave
+    // simply takes fewer rows
+    auto grab = [&]() -> int32_t {
+        uint32_t t = 0;
+        if (c.lane == 0)
+            t = __hip_atomic_fetch_add(&flags[kFlagTask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return (int32_t)__builtin_amdgcn_readfirstlane(t);
+    };
     uint32_t w[4][8];
-    Row cur = row_info(p.lay, prod);
-    if (cur.valid && !cur.scale) load_half(p, c.pg, cur, 0, w);
+    int32_t t = grab();
+    Row cur = row_info(p.lay, t);
+    if (cur.valid) load_half(p, c.pg, cur, 0, w);
+    int32_t pending = -1;  // scale row whose store completion is not yet published
 #pragma unroll 1
-    for (int32_t r = prod; r < total; r += kProducerWaves) {
-        const Row nxt = row_info(p.lay, r + kProducerWaves);
-        const bool prefetch = nxt.valid && !nxt.scale;
-        if (cur.scale)
-            scale_row(c, cur, nxt, prefetch, w);
-        else if (cur.s.kind == kSecInt8)
-            code_row<DT, kSecInt8>(c, cur, nxt, prefetch, w);
+    while (t < total) {
+        if (pending >= 0) {  // the wave waits for this row's prefetched groups here anyway
+            publish_scale(flags, pending);
+            pending = -1;
+        }
+        const int32_t tn = grab();
+        const Row nxt = row_info(p.lay, tn);
+        if (cur.s.kind == kSecInt8)
+            code_row<DT, kSecInt8>(c, cur, nxt, nxt.valid, w);
         else if (cur.s.kind == kSecInt4)
-            code_row<DT, kSecInt4>(c, cur, nxt, prefetch, w);
+            code_row<DT, kSecInt4>(c, cur, nxt, nxt.valid, w);
         else
-            code_row<DT, kSecRaw>(c, cur, nxt, prefetch, w);
+            code_row<DT, kSecRaw>(c, cur, nxt, nxt.valid, w);
+        if (cur.s.kind != kSecRaw) {
+            // count the unit's staged code rows; whoever stages the last one
+            // encrypts the unit's scales
+            uint32_t old = 0;
+            if (c.lane == 0)
+                old = __hip_atomic_fetch_add(&flags[kFlagCount + cur.g % kStage], 1u, __ATOMIC_ACQ_REL,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP);
+            old = __builtin_amdgcn_readfirstlane(old);
+            if (old == (uint32_t)cur.s.nblk - 1u) {
+                scale_row(c, cur);
+                pending = cur.g;
+            }
+        }
+        t = tn;
         cur = nxt;
     }
+    if (pending >= 0) publish_scale(flags, pending);
 }
 
 // The MAC wave's view of the payload: each section's code rows (LDS ring),
@@ -348,12 +396,12 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, in
 struct MacFeed {
     int32_t si, phase, i;
     int32_t cidx;
-    int32_t row_begin, code_begin, qunit_begin;
+    int32_t code_begin, qunit_begin;
 
     __device__ __forceinline__ void fetch(const EgressParams& p, const uint8_t* pay, const uint32_t* lds,
                                           int lane, uint4 (&x)[4], int32_t& tag) {
         const uint32_t* flags = lds + kLdsFlags;
-        const SecRows s = sec_rows(p.lay, si, row_begin, code_begin, qunit_begin);
+        const SecRows s = sec_rows(p.lay, si, code_begin, qunit_begin);
         if (phase == 0) {
             const uint32_t* slot = lds + (cidx % kRing) * kRowWords;
             wait_ge(&flags[kFlagRing + cidx % kRing], cidx + 1, p.state);
@@ -367,14 +415,13 @@ struct MacFeed {
             }
         } else {
             const int32_t g = s.qunit_begin + i;
-            wait_ge(&flags[kFlagStage + g % kStage], g + 1, p.state);
+            wait_ge(&flags[kFlagScale + g % kScaleSlots], g + 1, p.state);
             const uint8_t* q = pay + s.s_off + 64u * (uint32_t)i;
             x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
             tag = 0;
             if (++i == s.n_units) phase = 2;
         }
         if (phase == 2) {  // next section
-            row_begin += s.n_units * s.rpu;
             code_begin += s.n_units * s.nblk;
             if (s.kind != kSecRaw) qunit_begin += s.n_units;
             ++si;
@@ -402,7 +449,7 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     s.absorb_words<4>(hdr);
     const uint8_t* pay = blob + kHeader;
     uint32_t* used = lds + kLdsFlags + kFlagMacUsed;
-    MacFeed feed{0, 0, 0, 0, 0, 0, 0};
+    MacFeed feed{0, 0, 0, 0, 0, 0};
     const int32_t total = total_rows(p.lay);
     // three chunks in flight: two fetched ahead of the one being absorbed; a
     // code row's ring slot is released once it has been absorbed
@@ -436,7 +483,7 @@ __global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParam
     extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
-    for (int i = threadIdx.x; i < kRing + kStage + 4; i += blockDim.x) lds[kLdsFlags + i] = 0u;
+    for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) lds[kLdsFlags + i] = 0u;
     if (threadIdx.x < 64) {
         uint64_t* blobs = reinterpret_cast<uint64_t*>(lds + kLdsBlobs);
         const int pg = (int)threadIdx.x < ppw ? (int)threadIdx.x : 0;
@@ -450,9 +497,7 @@ __global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParam
         return;
     }
     if ((wave & 3) == 0) return;  // leave the MAC wave's SIMD to it
-    const int prod = wave - 1 - (wave >> 2);
-    if (prod >= kProducerWaves) return;  // never: launched with kFusedWaves waves
-    egress_produce<DT>(p, page0, ppw, prod, lds);
+    egress_produce<DT>(p, page0, ppw, lds);
 }
 
 }  // namespace
