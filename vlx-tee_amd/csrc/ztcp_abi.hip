@@ -15,7 +15,6 @@ using namespace ztcp;
 
 namespace {
 
-constexpr int kMaxBatchFlags = 4096;
 
 struct DeviceCtx {
     DeviceState* state = nullptr;
@@ -191,17 +190,16 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
     p.head_dim = (int32_t)g->head_dim;
     p.blob_bytes = (uint32_t)blob_bytes;
     p.payload = (uint32_t)(blob_bytes - kHeader - kTag);
+    p.rope_dim = (int32_t)g->rope_dim;
+    p.has_v = mla ? 0 : 1;
     bool all_aligned = true;
-    int32_t units = -1;
-    bool same_units = true;
     for (int preset = 1; preset <= 3; ++preset) {
         for (int rm = 0; rm <= 2; ++rm) {
             const int i = (preset - 1) * 3 + rm;
-            build_layout(preset, rm, vecs, g->head_dim, g->rope_dim, !mla, p.lay[i]);
-            p.lay_ok[i] = p.payload >= p.lay[i].required ? 1 : 0;
-            all_aligned = all_aligned && p.lay[i].aligned;
-            if (units < 0) units = p.lay[i].n_units;
-            same_units = same_units && units == p.lay[i].n_units;
+            Layout lay;
+            build_layout(preset, rm, vecs, g->head_dim, g->rope_dim, !mla, lay);
+            if (p.payload >= lay.required) p.lay_ok |= 1u << i;
+            all_aligned = all_aligned && lay.aligned;
         }
     }
     p.key = key_words(keys);
@@ -214,13 +212,11 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
     p.state = ctx->state;
     p.ppw = pages_per_group(batch, ctx->cu_count);
 
-    const bool fast = all_aligned && same_units && blob_bytes % 16 == 0 &&
+    const bool fast = all_aligned && blob_bytes % 16 == 0 &&
                       (descs || (aligned16(blobs) && aligned16(out_k) && (mla || aligned16(out_v))));
     hipError_t e = launch_reset_fail(p.state, stream);
     if (e == hipSuccess) {
         if (fast) {
-            p.n_units = units;
-            p.n_batches = (p.ppw * units + 63) / 64;
             e = launch_ingress_fused(p, g->hot_dtype, stream);
             if (e == hipSuccess && !p.per_page) e = launch_ingress_finalize(p, stream);
         } else {

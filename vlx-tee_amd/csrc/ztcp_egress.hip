@@ -36,16 +36,14 @@
 // Requires every section to hold a multiple of 32 groups (Layout::aligned),
 // payload == required and 16-byte aligned pointers; otherwise the host routes
 // the call to the generic kernels.
-#include "ztcp_params.h"
+#include "ztcp_rows.h"
 
 namespace ztcp {
 
 namespace {
 
-constexpr uint32_t kSpinLimit = 1u << 20;  // about 30 ms of s_sleep(1)
 constexpr int kRing = 24;             // code rows between producers and the MAC wave
 constexpr int kStage = 8;             // units whose scales are staged at once
-constexpr int kRowWords = 64 * 16;    // one row: 64 pages x 16 words
 constexpr int kLdsStage = kRing * kRowWords;
 constexpr int kScaleSlots = 64;      // scale rows the MAC wave may still be waiting for
 constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
@@ -59,62 +57,6 @@ constexpr int kNumFlags = kFlagMacUsed + 4;
 constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byte aligned)
 constexpr int kLdsWords = kLdsBlobs + 2 * 64;
 static_assert(kLdsBlobs % 2 == 0, "blob table must be 8-byte aligned");
-
-// Word offset of quad q (16 bytes) of page `pg` inside a row slot.  The quad
-// index is XOR-swizzled by page so that lane-per-page accesses and the
-// transposed four-lanes-per-page accesses are both free of bank conflicts.
-__device__ __forceinline__ uint32_t quad_word(int pg, int q) {
-    return (uint32_t)(pg * 16 + ((q ^ ((pg >> 1) & 3)) << 2));
-}
-
-__device__ __forceinline__ uint4 lds_quad(const uint32_t* row, int pg, int q) {
-    return *reinterpret_cast<const uint4*>(row + quad_word(pg, q));
-}
-__device__ __forceinline__ void lds_put_quad(uint32_t* row, int pg, int q, uint4 x) {
-    *reinterpret_cast<uint4*>(row + quad_word(pg, q)) = x;
-}
-
-// Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
-__device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, DeviceState* st) {
-    if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
-    for (uint32_t spin = 0;; ++spin) {
-        __builtin_amdgcn_s_sleep(1);
-        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
-        if (spin >= kSpinLimit) {
-            atomicOr(&st->diag, kDiagEgressWait);
-            return;
-        }
-    }
-}
-
-__device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
-    __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Row geometry of one section (all values wave-uniform).
-struct SecRows {
-    int32_t kind, nblk, rpu, n_units;
-    int32_t code_begin;
-    int32_t qunit_begin;  // units of quantized sections before this one (staging order)
-    int32_t gpv, col, src;
-    uint32_t q_off, s_off;
-};
-
-__device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t code_begin, int32_t qunit_begin) {
-    SecRows s;
-    s.kind = ZTCP_SEC_FIELD(lay, si, kind);
-    s.nblk = s.kind == kSecInt8 ? 8 : (s.kind == kSecInt4 ? 4 : 16);
-    s.rpu = s.nblk + (s.kind != kSecRaw ? 1 : 0);
-    s.n_units = ZTCP_SEC_FIELD(lay, si, n_units);
-    s.code_begin = code_begin;
-    s.qunit_begin = qunit_begin;
-    s.gpv = ZTCP_SEC_FIELD(lay, si, gpv);
-    s.col = ZTCP_SEC_FIELD(lay, si, col);
-    s.src = ZTCP_SEC_FIELD(lay, si, src);
-    s.q_off = ZTCP_SEC_FIELD(lay, si, q_off);
-    s.s_off = ZTCP_SEC_FIELD(lay, si, s_off);
-    return s;
-}
 
 struct Row {
     int32_t valid;
@@ -154,16 +96,6 @@ __device__ __forceinline__ Row row_info(const Layout& lay, int32_t t) {
     return row;
 }
 
-__device__ __forceinline__ int32_t total_code_rows(const Layout& lay) {
-    int32_t t = 0;
-#pragma unroll
-    for (int si = 0; si < 3; ++si) {
-        if (si >= lay.n_sec) continue;
-        const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
-        t += ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16));
-    }
-    return t;
-}
 
 __device__ __forceinline__ int32_t total_rows(const Layout& lay) {
     int32_t t = 0;
@@ -277,7 +209,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     if constexpr (SW > 0) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
         uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
-        wait_ge(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
+        wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
 #pragma unroll
         for (int t = 0; t < SW; ++t) {
             const int wd = row.j * SW + t;  // logical scale word of this lane's page
@@ -287,7 +219,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     uint32_t ks[16];
     st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
     uint32_t* slot = c.lds + (row.cidx % kRing) * kRowWords;
-    wait_ge(&flags[kFlagMacUsed], row.cidx - kRing + 1, p.state);
+    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.cidx - kRing + 1, p.state);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad(slot, c.lane, q,
@@ -404,7 +336,7 @@ struct MacFeed {
         const SecRows s = sec_rows(p.lay, si, code_begin, qunit_begin);
         if (phase == 0) {
             const uint32_t* slot = lds + (cidx % kRing) * kRowWords;
-            wait_ge(&flags[kFlagRing + cidx % kRing], cidx + 1, p.state);
+            wait_ge<kDiagEgressWait>(&flags[kFlagRing + cidx % kRing], cidx + 1, p.state);
 #pragma unroll
             for (int q = 0; q < 4; ++q) x[q] = lds_quad(slot, lane, q);
             tag = cidx + 1;
@@ -415,7 +347,7 @@ struct MacFeed {
             }
         } else {
             const int32_t g = s.qunit_begin + i;
-            wait_ge(&flags[kFlagScale + g % kScaleSlots], g + 1, p.state);
+            wait_ge<kDiagEgressWait>(&flags[kFlagScale + g % kScaleSlots], g + 1, p.state);
             const uint8_t* q = pay + s.s_off + 64u * (uint32_t)i;
             x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
             tag = 0;

@@ -177,7 +177,7 @@ __global__ void ingress_generic_verify_kernel(IngressParams p, int32_t* status) 
     else {
         const uint32_t preset = flags & 0x0Fu, rope_mode = flags >> 4;
         if (preset < 1u || preset > 3u || rope_mode > 2u ||
-            !p.lay_ok[(preset - 1u) * 3u + rope_mode])
+            !((p.lay_ok >> ((preset - 1u) * 3u + rope_mode)) & 1u))
             st = 1;
     }
     status[page] = st;
@@ -198,8 +198,8 @@ __global__ void ingress_generic_decode_kernel(IngressParams p, int64_t groups_pe
         const uint32_t preset = flags & 0x0Fu, rope_mode = flags >> 4;
         if (preset < 1u || preset > 3u || rope_mode > 2u) continue;
         const int li = (int)((preset - 1u) * 3u + rope_mode);
-        if (!p.lay_ok[li]) continue;
-        const Layout& L = p.lay[li];
+        if (!((p.lay_ok >> li) & 1u)) continue;
+        const Layout L = ingress_layout(p, li);
         int si = 0;
         while (si < L.n_sec - 1 && gi >= L.sec[si].n_groups) gi -= L.sec[si++].n_groups;
         const Section S = L.sec[si];

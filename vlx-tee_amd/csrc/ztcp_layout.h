@@ -55,56 +55,63 @@ ZTCP_HD inline int32_t code_bytes_per_group(int32_t kind) {
     return kind == kSecInt8 ? 16 : (kind == kSecInt4 ? 8 : 32);
 }
 
+ZTCP_HD inline Section make_section(int32_t kind, int32_t src, int32_t col, int32_t width, int64_t vecs,
+                                   uint32_t off, int32_t units) {
+    Section s;
+    s.kind = kind;
+    s.src = src;
+    s.col = col;
+    s.gpv = width / 16;
+    s.n_groups = (int32_t)(vecs * s.gpv);
+    s.unit_begin = units;
+    s.n_units = (s.n_groups + 31) / 32;
+    s.q_off = off;
+    const uint32_t code = (uint32_t)s.n_groups * (uint32_t)code_bytes_per_group(kind);
+    s.s_off = off + code;
+    s.bytes = code + (kind == kSecRaw ? 0u : 2u * (uint32_t)s.n_groups);
+    return s;
+}
+
+// c ? x : y field by field (a select of whole structs would go through memory
+// on the device).
+ZTCP_HD inline Section pick(bool c, const Section& x, const Section& y) {
+    return Section{c ? x.kind : y.kind,         c ? x.src : y.src,         c ? x.col : y.col,
+                   c ? x.gpv : y.gpv,           c ? x.n_groups : y.n_groups,
+                   c ? x.unit_begin : y.unit_begin, c ? x.n_units : y.n_units,
+                   c ? x.q_off : y.q_off,       c ? x.s_off : y.s_off,     c ? x.bytes : y.bytes};
+}
+
 // Returns false for preset / rope_mode outside 1..3 / 0..2 (cpp:1447-1449).
-ZTCP_HD inline bool build_layout(int64_t preset, int64_t rope_mode, int64_t vecs,
-                                 int64_t head_dim, int64_t rope_dim, bool has_v, Layout& L) {
+// Written with selects only (no indexed stores), so that a Layout built on the
+// device from wave-uniform flags stays in scalar registers.
+ZTCP_HD inline bool build_layout(int64_t preset, int64_t rope_mode, int64_t vecs, int64_t head_dim,
+                                 int64_t rope_dim, bool has_v, Layout& L) {
     if (preset < 1 || preset > 3 || rope_mode < 0 || rope_mode > 2) return false;
-    int32_t kinds[3], srcs[3], cols[3], widths[3];
-    int n = 0;
-    if (rope_mode == 2 && rope_dim > 0) {
-        kinds[n] = kSecRaw; srcs[n] = 0; cols[n] = 0; widths[n] = (int32_t)rope_dim; ++n;
-    } else if (rope_mode == 1 && rope_dim > 0) {
-        kinds[n] = kSecInt8; srcs[n] = 0; cols[n] = 0; widths[n] = (int32_t)rope_dim; ++n;
-    }
+    // candidate sections in payload order: K RoPE columns, the other K columns, V
+    const bool pa = rope_mode != 0 && rope_dim > 0;
     const int64_t kq = rope_mode == 0 ? head_dim : head_dim - rope_dim;
-    const int64_t kc = rope_mode == 0 ? 0 : rope_dim;
-    if (kq > 0) {
-        kinds[n] = preset == 1 ? kSecInt4 : kSecInt8; srcs[n] = 0;
-        cols[n] = (int32_t)kc; widths[n] = (int32_t)kq; ++n;
-    }
-    if (has_v) {
-        kinds[n] = (preset == 1 || preset == 2) ? kSecInt4 : kSecInt8; srcs[n] = 1;
-        cols[n] = 0; widths[n] = (int32_t)head_dim; ++n;
-    }
-    uint32_t off = 0;
-    int32_t units = 0;
-    bool aligned = true;
-    for (int i = 0; i < 3; ++i) {
-        Section& s = L.sec[i];
-        if (i >= n) {
-            s = Section{kSecInt8, 0, 0, 0, 0, units, 0, off, off, 0};
-            continue;
-        }
-        s.kind = kinds[i];
-        s.src = srcs[i];
-        s.col = cols[i];
-        s.gpv = widths[i] / 16;
-        s.n_groups = (int32_t)(vecs * s.gpv);
-        s.unit_begin = units;
-        s.n_units = (s.n_groups + 31) / 32;
-        s.q_off = off;
-        const uint32_t code = (uint32_t)s.n_groups * (uint32_t)code_bytes_per_group(s.kind);
-        const uint32_t scales = s.kind == kSecRaw ? 0u : 2u * (uint32_t)s.n_groups;
-        s.s_off = off + code;
-        s.bytes = code + scales;
-        off += s.bytes;
-        units += s.n_units;
-        if (s.n_groups % 32 != 0) aligned = false;
-    }
-    L.n_sec = n;
+    const bool pb = kq > 0, pc = has_v;
+    const Section a = make_section(rope_mode == 2 ? kSecRaw : kSecInt8, 0, 0, pa ? (int32_t)rope_dim : 0, vecs, 0u, 0);
+    const uint32_t off_b = pa ? a.bytes : 0u;
+    const int32_t units_b = pa ? a.n_units : 0;
+    const Section b = make_section(preset == 1 ? kSecInt4 : kSecInt8, 0, rope_mode == 0 ? 0 : (int32_t)rope_dim,
+                                   pb ? (int32_t)kq : 0, vecs, off_b, units_b);
+    const uint32_t off_c = off_b + (pb ? b.bytes : 0u);
+    const int32_t units_c = units_b + (pb ? b.n_units : 0);
+    const Section c = make_section((preset == 1 || preset == 2) ? kSecInt4 : kSecInt8, 1, 0,
+                                   pc ? (int32_t)head_dim : 0, vecs, off_c, units_c);
+    const uint32_t end = off_c + (pc ? c.bytes : 0u);
+    const int32_t units = units_c + (pc ? c.n_units : 0);
+    const Section e{kSecInt8, 0, 0, 0, 0, units, 0, end, end, 0};  // unused slot
+    const Section c_or_e = pick(pc, c, e);
+    const Section b_or_c = pick(pb, b, c_or_e);
+    L.sec[0] = pick(pa, a, b_or_c);
+    L.sec[1] = pick(pa, b_or_c, pick(pb && pc, c, e));
+    L.sec[2] = pick(pa && pb && pc, c, e);
+    L.n_sec = (pa ? 1 : 0) + (pb ? 1 : 0) + (pc ? 1 : 0);
     L.n_units = units;
-    L.required = off;
-    L.aligned = aligned ? 1 : 0;
+    L.required = end;
+    L.aligned = (!pa || a.n_groups % 32 == 0) && (!pb || b.n_groups % 32 == 0) && (!pc || c.n_groups % 32 == 0);
     return true;
 }
 

@@ -19,7 +19,8 @@ constexpr int kFusedThreads = 64 * kFusedWaves;
 constexpr int kProducerWaves = kFusedWaves - 1 - (kFusedWaves - 1) / 4;
 
 // Sticky device diagnostics (bit flags, or-ed by kernels).
-constexpr uint32_t kDiagEgressWait = 1u;   // MAC wave's bounded wait expired
+constexpr uint32_t kDiagEgressWait = 1u;   // a bounded wait of the fused egress kernel expired
+constexpr uint32_t kDiagIngressWait = 2u;  // a bounded wait of the fused ingress kernel expired
 
 // Per-device library state (allocated once per device by the host side).
 struct DeviceState {
@@ -63,16 +64,15 @@ struct IngressParams {
     int32_t vecs, head_dim;
     uint32_t blob_bytes;
     uint32_t payload;              // blob_bytes - 48
-    Layout lay[9];                 // layout for preset 1..3 x rope_mode 0..2
-    int32_t lay_ok[9];             // flags valid and payload >= required
-    int32_t n_units;               // the same for every valid flag combination
+    int32_t rope_dim, has_v;       // geometry of the page layouts (ingress_layout)
+    uint32_t lay_ok;               // bit (preset - 1) * 3 + rope_mode: payload >= required
+    int32_t n_units;               // generic path: 16-element groups per page
     ChaKey key;
     uint64_t mk0, mk1;
     uint32_t exp_tenant, exp_model;
     uint32_t exp_layer;
     int32_t per_page;              // zero failing pages in-kernel
     int32_t ppw;
-    int32_t n_batches;
     DeviceState* state;
 };
 
@@ -108,6 +108,14 @@ __device__ __forceinline__ EgressPage egress_page(const EgressParams& p, int64_t
         e.nonce2 = p.nonce2;
     }
     return e;
+}
+
+// Layout of header flags index li = (preset - 1) * 3 + rope_mode, computed
+// in registers (no table in the kernel arguments).
+__device__ __forceinline__ Layout ingress_layout(const IngressParams& p, int li) {
+    Layout L;
+    build_layout(li / 3 + 1, li % 3, p.vecs, p.head_dim, p.rope_dim, p.has_v != 0, L);
+    return L;
 }
 
 __device__ __forceinline__ const uint8_t* ingress_blob(const IngressParams& p, int64_t page) {

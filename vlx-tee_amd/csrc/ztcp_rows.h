@@ -1,0 +1,87 @@
+// ztcp_rows.h -- row geometry and LDS hand-off helpers shared by the fused
+// egress and ingress kernels.
+//
+// A row is one 64-byte keystream block position of the payload, for all pages
+// of a workgroup (lane = page).  Row slots in LDS hold 16 words per page; the
+// 16-byte quads of a page are XOR-swizzled so that both lane-per-page access
+// and the transposed four-lanes-per-page access used for coalesced global
+// stores are free of bank conflicts.
+#pragma once
+
+#include "ztcp_params.h"
+
+namespace ztcp {
+
+constexpr uint32_t kSpinLimit = 1u << 20;  // about 30 ms of s_sleep(1)
+constexpr int kRowWords = 64 * 16;         // one row: 64 pages x 16 words
+
+// Word offset of quad q (16 bytes) of page `pg` inside a row slot.  The quad
+// index is XOR-swizzled by page so that lane-per-page accesses and the
+// transposed four-lanes-per-page accesses are both free of bank conflicts.
+__device__ __forceinline__ uint32_t quad_word(int pg, int q) {
+    return (uint32_t)(pg * 16 + ((q ^ ((pg >> 1) & 3)) << 2));
+}
+
+__device__ __forceinline__ uint4 lds_quad(const uint32_t* row, int pg, int q) {
+    return *reinterpret_cast<const uint4*>(row + quad_word(pg, q));
+}
+__device__ __forceinline__ void lds_put_quad(uint32_t* row, int pg, int q, uint4 x) {
+    *reinterpret_cast<uint4*>(row + quad_word(pg, q)) = x;
+}
+
+// Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
+// Bounded: an expired wait sets the sticky diagnostic bit DIAG and returns.
+template <uint32_t DIAG>
+__device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, DeviceState* st) {
+    if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
+    for (uint32_t spin = 0;; ++spin) {
+        __builtin_amdgcn_s_sleep(1);
+        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
+        if (spin >= kSpinLimit) {
+            atomicOr(&st->diag, DIAG);
+            return;
+        }
+    }
+}
+
+__device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
+    __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Row geometry of one section (all values wave-uniform).
+struct SecRows {
+    int32_t kind, nblk, rpu, n_units;
+    int32_t code_begin;
+    int32_t qunit_begin;  // units of quantized sections before this one (staging order)
+    int32_t gpv, col, src;
+    uint32_t q_off, s_off;
+};
+
+__device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t code_begin, int32_t qunit_begin) {
+    SecRows s;
+    s.kind = ZTCP_SEC_FIELD(lay, si, kind);
+    s.nblk = s.kind == kSecInt8 ? 8 : (s.kind == kSecInt4 ? 4 : 16);
+    s.rpu = s.nblk + (s.kind != kSecRaw ? 1 : 0);
+    s.n_units = ZTCP_SEC_FIELD(lay, si, n_units);
+    s.code_begin = code_begin;
+    s.qunit_begin = qunit_begin;
+    s.gpv = ZTCP_SEC_FIELD(lay, si, gpv);
+    s.col = ZTCP_SEC_FIELD(lay, si, col);
+    s.src = ZTCP_SEC_FIELD(lay, si, src);
+    s.q_off = ZTCP_SEC_FIELD(lay, si, q_off);
+    s.s_off = ZTCP_SEC_FIELD(lay, si, s_off);
+    return s;
+}
+
+__device__ __forceinline__ int32_t total_code_rows(const Layout& lay) {
+    int32_t t = 0;
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= lay.n_sec) continue;
+        const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
+        t += ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16));
+    }
+    return t;
+}
+
+}  // namespace ztcp
