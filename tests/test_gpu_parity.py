@@ -130,6 +130,37 @@ def test_padded_payload_generic_path(hip, O, pad):
     assert np.array_equal(gk, ok) and np.array_equal(gv, ov)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("first_bad", [False, True])
+def test_mixed_layouts_in_one_batch(hip, O, dtype, first_bad):
+    """One ingress batch whose pages carry different header flags (each page
+    decodes under its own preset / rope mode, cpp:2340-2341), padded to one
+    blob size; optionally the first page's flags are invalid, so another page
+    sets the workgroup's layout."""
+    T, Hh, D, R, mla, B = 16, 4, 128, 64, False, 520  # > 256 pages: several pages per workgroup
+    k, v = _pages(29, B, T, Hh, D, R, mla, DT[dtype])
+    th = np.arange(B, dtype=np.int64) * 31 + 5
+    combos = [(3, 0), (1, 1), (2, 2), (1, 0), (2, 1), (3, 1)]
+    exp = max(O.payload_bytes(p, rm, T * Hh, D, R, True) for p, rm in combos)
+    blobs = np.zeros((B, 48 + exp), dtype=np.uint8)
+    kb, vb = _bits(k), _bits(v)
+    for i in range(B):
+        p, rm = combos[(i * 5) % len(combos)]
+        blobs[i] = O.egress_batch(kb[i:i + 1], vb[i:i + 1], th[i:i + 1], dtype=_odt(O, DT[dtype]), preset=p,
+                                  rope_mode=rm, rope_dim=R, expected_payload_bytes=exp, tenant_id_hash=TEN,
+                                  model_id_hash=MOD, layer_id=LAYER, head_group_id=HG,
+                                  base_sequence_nonce=BASE + i, **KEYS)[0]
+    if first_bad:
+        blobs[0, 3] = 0x07  # flags byte: preset 7 (invalid); fails the MAC first
+    print(f"case mixed layouts {dtype} first_bad={first_bad}", flush=True)
+    err, st, gk, gv, rc, ost, ok, ov = _ingress_both(hip, O, blobs, th, T, Hh, D, R, mla, DT[dtype],
+                                                      per_page=True)
+    assert np.array_equal(st, ost)
+    assert (st[1:] == 0).all() and st[0] == (3 if first_bad else 0)
+    assert np.array_equal(gk, ok) and np.array_equal(gv, ov)
+    assert hip.device_diag() == 0
+
+
 @pytest.mark.parametrize("per_page", [False, True])
 def test_tamper_matrix(hip, O, per_page):
     """bench_cold_page_pipeline.py:318-401 on the GPU path, plus header cases."""
