@@ -55,7 +55,8 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
 
     _package().load_native()
     import vlx_tee_amd.pages as P
-    from vlx_tee_amd.workloads import MODEL_HASH, TENANT_HASH, WORKLOADS, generate, page_metadata, session_keys
+    from vlx_tee_amd.workloads import (MODEL_HASH, TENANT_HASH, WORKLOADS, generate, page_metadata,
+                                       session_keys, tamper_plan)
 
     w = WORKLOADS[wname]
     dev = torch.device("cuda:0")
@@ -68,7 +69,11 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
     vo = None if v is None else torch.empty_like(v)
     status = torch.full((w.n_pages,), -1, dtype=torch.int32, device=dev)
     d_out = P.build_descriptors(k, v, blobs, th, seq, layers)
-    d_in = P.build_descriptors(ko, vo, blobs, th, seq, layers)
+    # tamper workloads: ingress reads a copy of the blobs with one bit flipped
+    # in a seeded 1% of pages, under the per-page policy (failing pages zeroed)
+    t_pages, t_bits = tamper_plan(w, w.blob_bytes)
+    blobs_in = blobs.clone() if len(t_pages) else blobs
+    d_in = P.build_descriptors(ko, vo, blobs_in, th, seq, layers)
     geo = dict(num_tokens=w.num_tokens, num_heads=w.num_heads, head_dim=w.head_dim,
                rope_dim=w.rope_dim, dtype=torch.bfloat16, is_mla_single_buffer=w.mla)
 
@@ -79,15 +84,29 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
 
     def ingress():
         P.ingress(d_in, w.n_pages, w.blob_bytes, expected_tenant_hash=TENANT_HASH,
-                  expected_model_hash=MODEL_HASH, page_status=status, asynchronous=True, **geo, **keys)
+                  expected_model_hash=MODEL_HASH, page_status=status, asynchronous=True,
+                  per_page=bool(len(t_pages)), **geo, **keys)
 
+    want_status = np.zeros(w.n_pages, dtype=np.int32)
+    if len(t_pages):
+        egress()
+        blobs_in.copy_(blobs)
+        idx = torch.from_numpy(t_pages).to(dev)
+        cols = torch.from_numpy(t_bits // 8).to(dev)
+        blobs_in[idx, cols] = blobs_in[idx, cols] ^ torch.from_numpy((1 << (t_bits % 8)).astype(np.uint8)).to(dev)
+        want_status[t_pages] = -1  # any rejection verdict
     for _ in range(warmup):
         egress()
         ingress()
     torch.cuda.synchronize()
-    st = status.cpu().numpy()
-    if not (st == 0).all():
-        raise SystemExit(f"bench: {int((st != 0).sum())} pages failed verification after warmup")
+
+    def check_status(when):
+        st = status.cpu().numpy()
+        bad = (st != 0) != (want_status != 0)
+        if bad.any():
+            raise SystemExit(f"bench: {int(bad.sum())} pages with the wrong verdict {when}")
+
+    check_status("after warmup")
     # self-consistency: a second encode reproduces the blobs bit for bit
     ref_blobs = blobs.clone()
     egress()
@@ -114,9 +133,7 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
     wall = time.perf_counter() - t0
     te = [a.elapsed_time(b) for a, b, _ in ev]
     ti = [b.elapsed_time(c) for _, b, c in ev]
-    st = status.cpu().numpy()
-    if not (st == 0).all():
-        raise SystemExit("bench: pages failed verification in the timed region")
+    check_status("in the timed region")
     hot = w.n_pages * w.hot_bytes_per_page
     wire = w.n_pages * w.blob_bytes
     me, mi = statistics.mean(te), statistics.mean(ti)
@@ -129,9 +146,10 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
         roundtrip_hot_gbps=2 * hot / (me + mi) / 1e6,
         egress_hbm_frac=(hot + wire) / me / 1e6 / HBM_PEAK_GBPS,
         ingress_hbm_frac=(hot + wire) / mi / 1e6 / HBM_PEAK_GBPS,
+        tampered_pages_rejected=f"{len(t_pages)}/{len(t_pages)}" if len(t_pages) else None,
         device_diag=diag,
     )
-    del k, v, blobs, ko, vo
+    del k, v, blobs, blobs_in, ko, vo
     torch.cuda.empty_cache()
     return res
 
@@ -233,7 +251,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c2_k8v4_prefix1g")
-    ap.add_argument("--also", default="c2_int4_prefix1g", help="comma list of extra workloads")
+    ap.add_argument("--also", default="c2_int4_prefix1g,c3_fp8only_tamper,c4_mla_int4",
+                    help="comma list of extra workloads")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
