@@ -134,14 +134,17 @@ __device__ __forceinline__ void load_half(const EgressParams& p, const EgressPag
 
 // Stores one row slot to the blobs: lane l writes quad (l & 3) of page
 // 16 k + (l >> 2), so each store instruction writes 64 contiguous bytes of 16
-// pages.  tb[k] is that page's blob pointer (null past the last page).
-__device__ __forceinline__ void store_row(const uint32_t* slot, uint8_t* const (&tb)[4], uint32_t blob_off,
+// pages.  The blob pointers come from the workgroup's LDS table (null past
+// the last page).
+__device__ __forceinline__ void store_row(const uint32_t* slot, const uint32_t* lds, uint32_t blob_off,
                                           int lane) {
+    const uint64_t* blobs = reinterpret_cast<const uint64_t*>(lds + kLdsBlobs);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int pr = 16 * k + (lane >> 2), q = lane & 3;
         const uint4 x = lds_quad(slot, pr, q);
-        if (tb[k]) stg16(tb[k] + blob_off, q, x);
+        uint8_t* b = reinterpret_cast<uint8_t*>(blobs[pr]);
+        if (b) stg16(b + blob_off, q, x);
     }
 }
 
@@ -149,8 +152,8 @@ struct ProducerCtx {
     const EgressParams* p;
     EgressPage pg;
     uint32_t n0, n1, n2;
+    ChaChaNonceCache nc;
     uint32_t* lds;
-    uint8_t* tb[4];
     int lane;
 };
 
@@ -185,7 +188,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     uint32_t pt[16];
     uint32_t sc[4];
     ChaChaState st;
-    st.start(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2);
+    st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
     if constexpr (KIND == kSecRaw) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -193,15 +196,15 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
             pt[8 + t] = w[1][t];
         }
         if (prefetch) load_half(p, c.pg, nxt, 0, w);
-        st.double_rounds<10>();
+        st.double_rounds<9>();
     } else if constexpr (KIND == kSecInt8) {
         quant_half<DT, 8>(w, pt, sc);
         if (prefetch) load_half(p, c.pg, nxt, 0, w);
-        st.double_rounds<10>();
+        st.double_rounds<9>();
     } else {
         quant_half<DT, 4>(w, pt, sc);
         load_half(p, c.pg, row, 1, w);
-        st.double_rounds<5>();
+        st.double_rounds<4>();
         quant_half<DT, 4>(w, pt + 8, sc + 2);
         if (prefetch) load_half(p, c.pg, nxt, 0, w);
         st.double_rounds<5>();
@@ -225,7 +228,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         lds_put_quad(slot, c.lane, q,
                      make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
                                 pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
-    store_row(slot, c.tb, (uint32_t)kHeader + 64u * (uint32_t)row.block, c.lane);
+    store_row(slot, c.lds, (uint32_t)kHeader + 64u * (uint32_t)row.block, c.lane);
     publish(&flags[kFlagRing + row.cidx % kRing], (uint32_t)row.cidx + 1u);
 }
 
@@ -238,7 +241,7 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) 
     uint32_t* flags = c.lds + kLdsFlags;
     const uint32_t block = row.s.s_off / 64u + (uint32_t)row.u;
     uint32_t ks[16];
-    chacha_block(p.key, 1u + block, c.n0, c.n1, c.n2, ks);
+    chacha_block_cached(p.key, c.nc, 1u + block, c.n0, c.n1, c.n2, ks);
     uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -246,7 +249,7 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) 
         lds_put_quad(stage, c.lane, q,
                      make_uint4(s.x ^ ks[4 * q], s.y ^ ks[4 * q + 1], s.z ^ ks[4 * q + 2], s.w ^ ks[4 * q + 3]));
     }
-    store_row(stage, c.tb, (uint32_t)kHeader + 64u * block, c.lane);
+    store_row(stage, c.lds, (uint32_t)kHeader + 64u * block, c.lane);
     flags[kFlagCount + row.g % kStage] = 0u;
     publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
 }
@@ -267,13 +270,8 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     c.n0 = (uint32_t)c.pg.seq;
     c.n1 = (uint32_t)(c.pg.seq >> 32);
     c.n2 = c.pg.nonce2;
+    c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
-    const uint64_t* blobs = reinterpret_cast<const uint64_t*>(lds + kLdsBlobs);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int pr = 16 * k + (c.lane >> 2);
-        c.tb[k] = pr < ppw ? reinterpret_cast<uint8_t*>(blobs[pr]) : nullptr;
-    }
     const int32_t total = total_code_rows(p.lay);
     uint32_t* flags = lds + kLdsFlags;
     // code rows are handed out in order from an LDS counter, one row ahead of
@@ -418,8 +416,8 @@ __global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParam
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) lds[kLdsFlags + i] = 0u;
     if (threadIdx.x < 64) {
         uint64_t* blobs = reinterpret_cast<uint64_t*>(lds + kLdsBlobs);
-        const int pg = (int)threadIdx.x < ppw ? (int)threadIdx.x : 0;
-        blobs[threadIdx.x] = reinterpret_cast<uint64_t>(egress_page(p, page0 + pg).blob);
+        blobs[threadIdx.x] = (int)threadIdx.x < ppw ? reinterpret_cast<uint64_t>(egress_page(p, page0 + threadIdx.x).blob)
+                                                    : 0ull;  // no stores past the last page
     }
     __syncthreads();
     const int wave = threadIdx.x >> 6;

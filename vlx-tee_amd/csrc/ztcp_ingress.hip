@@ -261,6 +261,7 @@ struct DecoderCtx {
     const IngressParams* p;
     const uint8_t* pay;     // this lane's page payload
     uint32_t n0, n1, n2;    // this lane's page nonce (from its header)
+    ChaChaNonceCache nc;
     uint32_t* lds;
     uint32_t* tile;         // this wave's dequantized tile
     int lane;
@@ -298,7 +299,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     uint32_t pt[16];
     {
         uint32_t ks[16];
-        chacha_block(p.key, 1u + (uint32_t)k.block, c.n0, c.n1, c.n2, ks);
+        chacha_block_cached(p.key, c.nc, 1u + (uint32_t)k.block, c.n0, c.n1, c.n2, ks);
 #pragma unroll
         for (int i = 0; i < 16; ++i) pt[i] = ct[i] ^ ks[i];
     }
@@ -354,7 +355,7 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
     uint32_t sc[16];
     {
         uint32_t ks[16];
-        chacha_block(p.key, 1u + (uint32_t)k.block, c.n0, c.n1, c.n2, ks);
+        chacha_block_cached(p.key, c.nc, 1u + (uint32_t)k.block, c.n0, c.n1, c.n2, ks);
 #pragma unroll
         for (int i = 0; i < 16; ++i) sc[i] = ct[i] ^ ks[i];
     }
@@ -531,6 +532,7 @@ __global__ __launch_bounds__(kFusedThreads) void ingress_fused_kernel(IngressPar
         c.n0 = h1.z;  // nonce from the page's own header (cpp:2357-2365)
         c.n1 = h1.w;
         c.n2 = ((h0.w & 0xFFFFu) << 16) | (h0.w >> 16);
+        c.nc.init(p.key, c.n0, c.n1, c.n2);
         c.lds = lds;
         c.tile = lds + kLdsTile + (wave - 1 - (wave >> 2)) * kRowWords;
         c.lane = lane;

@@ -29,6 +29,23 @@ __device__ __forceinline__ void lds_put_quad(uint32_t* row, int pg, int q, uint4
     *reinterpret_cast<uint4*>(row + quad_word(pg, q)) = x;
 }
 
+// Byte offsets of the four quads of one page inside a row slot, computed once
+// per lane (the swizzle depends only on the page).
+struct PageQuads {
+    uint32_t off[4];
+    __device__ __forceinline__ void init(int pg) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) off[q] = quad_word(pg, q) * 4u;
+    }
+};
+
+__device__ __forceinline__ uint4 lds_quad_at(const uint32_t* row, uint32_t byte_off) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(row) + byte_off);
+}
+__device__ __forceinline__ void lds_put_quad_at(uint32_t* row, uint32_t byte_off, uint4 x) {
+    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(row) + byte_off) = x;
+}
+
 // Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
 // Bounded: an expired wait sets the sticky diagnostic bit DIAG and returns.
 template <uint32_t DIAG>
