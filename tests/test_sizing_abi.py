@@ -66,12 +66,13 @@ def test_required_vs_padded(pkg, O):
                 assert N.lib().ztcp_payload_bytes(C.byref(g), preset, rm) == (req + 3) & ~3
 
 
-def test_library_exports_every_declared_symbol(pkg):
+@pytest.mark.parametrize("header,exports", [("ztcp.h", "EXPORTS"), ("ztcp_keyring.h", "KEYRING_EXPORTS")])
+def test_library_exports_every_declared_symbol(pkg, header, exports):
     import vlx_tee_amd._native as N
 
-    header = (REPO / "include" / "ztcp.h").read_text()
-    declared = set(re.findall(r"^\s*(?:[\w\*\s]+?)\b(ztcp_\w+)\s*\(", header, flags=re.M))
-    assert declared == set(N.EXPORTS), declared ^ set(N.EXPORTS)
+    text = (REPO / "include" / header).read_text()
+    declared = set(re.findall(r"^\s*(?:[\w\*\s]+?)\b(ztcp_\w+)\s*\(", text, flags=re.M))
+    assert declared == set(getattr(N, exports)), declared ^ set(getattr(N, exports))
     lib = N.lib()
     for name in declared:
         assert hasattr(lib, name), name

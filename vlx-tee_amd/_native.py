@@ -1,4 +1,5 @@
-"""ctypes binding of the HIP C-ABI library (include/ztcp.h -> libztcp_hip.so).
+"""ctypes binding of the C-ABI library (include/ztcp.h and include/ztcp_keyring.h
+-> libztcp_hip.so).
 
 The library is loaded after ``torch`` so both share torch's HIP runtime (the
 library's DT_NEEDED ``libamdhip64.so.7`` resolves to the copy torch already
@@ -27,6 +28,21 @@ EXPORTS = (
     "ztcp_chacha20_xor", "ztcp_siphash128",
     "ztcp_selftest", "ztcp_device_diag", "ztcp_strerror",
 )
+
+# Every symbol include/ztcp_keyring.h declares (host code, callable without a GPU).
+KEYRING_EXPORTS = (
+    "ztcp_keyring_create", "ztcp_keyring_destroy", "ztcp_keyring_derive_or_get",
+    "ztcp_keyring_derive_with_secret_for_test", "ztcp_keyring_next_sequence_nonce",
+    "ztcp_keyring_preflight_egress", "ztcp_keyring_begin_egress", "ztcp_keyring_commit_egress",
+    "ztcp_keyring_release_reservation", "ztcp_reservation_last_sequence",
+    "ztcp_reservation_generation", "ztcp_keyring_begin_ingress", "ztcp_keyring_verify_freshness",
+    "ztcp_keyring_verify_freshness_batch", "ztcp_keyring_finish_ingress",
+    "ztcp_keyring_shred_session", "ztcp_keyring_shred_tenant", "ztcp_keyring_last_error",
+    "ztcp_sha256", "ztcp_hmac_sha256",
+)
+
+# Key-ring return codes (include/ztcp_keyring.h).
+KR_EINVAL, KR_ESTALE, KR_ENONCE, KR_ESHREDDED, KR_ENOMEM, KR_ERANDOM = -1, -10, -11, -12, -13, -14
 
 
 class Geometry(C.Structure):
@@ -88,8 +104,41 @@ def lib() -> C.CDLL:
     L.ztcp_device_diag.restype = i32
     L.ztcp_strerror.argtypes = [i32]
     L.ztcp_strerror.restype = C.c_char_p
+    _bind_keyring(L)
     _lib = L
     return L
+
+
+def _bind_keyring(L: C.CDLL) -> None:
+    P, S, B, SZ = C.c_void_p, C.c_char_p, C.c_char_p, C.c_size_t
+    u64, u32, u16, i32 = C.c_uint64, C.c_uint32, C.c_uint16, C.c_int
+    PP, PU64 = C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)
+    sig = {
+        "ztcp_keyring_create": ([B, SZ, PP], i32),
+        "ztcp_keyring_destroy": ([P], None),
+        "ztcp_keyring_derive_or_get": ([P, S, S, P, P, PU64], i32),
+        "ztcp_keyring_derive_with_secret_for_test": ([P, S, S, B, P, P, PU64], i32),
+        "ztcp_keyring_next_sequence_nonce": ([P, S, S, u64, PU64], i32),
+        "ztcp_keyring_preflight_egress": ([P, S, S, u32, u16, u16, u64, P, SZ, PP], i32),
+        "ztcp_keyring_begin_egress": ([P, S, S, P, P, P], i32),
+        "ztcp_keyring_commit_egress": ([P, S, S, P], i32),
+        "ztcp_keyring_release_reservation": ([P, S, S, P], None),
+        "ztcp_reservation_last_sequence": ([P], u64),
+        "ztcp_reservation_generation": ([P], u64),
+        "ztcp_keyring_begin_ingress": ([P, S, S, PU64, P, P], i32),
+        "ztcp_keyring_verify_freshness": ([P, S, S, u32, u16, u16, u64, u64, PU64, PU64, PU64], i32),
+        "ztcp_keyring_verify_freshness_batch": ([P, S, S, P, SZ, PU64, PU64], i32),
+        "ztcp_keyring_finish_ingress": ([P, S, S, u64], i32),
+        "ztcp_keyring_shred_session": ([P, S, S], i32),
+        "ztcp_keyring_shred_tenant": ([P, S], i32),
+        "ztcp_keyring_last_error": ([], C.c_char_p),
+        "ztcp_sha256": ([B, SZ, P], None),
+        "ztcp_hmac_sha256": ([B, SZ, B, SZ, P], None),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
 
 
 def strerror(code: int) -> str:

@@ -1,7 +1,9 @@
 """Build the HIP C-ABI library ``libztcp_hip.so`` in-tree for gfx950.
 
-``python vlx-tee_amd/build.py`` compiles every ``csrc/*.hip`` with hipcc into
-``vlx-tee_amd/libztcp_hip.so`` (exported symbols: include/ztcp.h).
+``python vlx-tee_amd/build.py`` compiles every ``csrc/*.hip`` (device code)
+and ``csrc/*.cpp`` (host code: the session key ring) with hipcc into
+``vlx-tee_amd/libztcp_hip.so`` (exported symbols: include/ztcp.h and
+include/ztcp_keyring.h).
 
 Flags: ``-ffp-contract=off`` and no fast-math (the quantizer's fp32 rounding
 order must match the reference's), packed-FP32 instructions disabled.
@@ -26,7 +28,7 @@ HIPCC_FLAGS = [
 
 
 def sources() -> list[Path]:
-    return sorted((HERE / "csrc").glob("*.hip"))
+    return sorted((HERE / "csrc").glob("*.hip")) + sorted((HERE / "csrc").glob("*.cpp"))
 
 
 def build(verbose: bool = False) -> Path:

@@ -1,9 +1,9 @@
 """Wire-format constants and payload sizing of a cold page.
 
-Mirror of research/baseline_codec/cold_page_spec.py (spec:47-67, spec:117-161,
-spec:164-253): the 32-byte little-endian header, presets, RoPE modes and the
-payload size (padded to 4 bytes) the reference's Python wrapper passes as
-``expected_payload_bytes``.
+Mirror of research/baseline_codec/cold_page_spec.py (spec:47-67, spec:83-161,
+spec:164-253): the 32-byte little-endian header, the AAD record bound to it,
+presets, RoPE modes and the payload size (padded to 4 bytes) the reference's
+Python wrapper passes as ``expected_payload_bytes``.
 """
 from __future__ import annotations
 
@@ -48,6 +48,48 @@ def unpack_header(b: bytes) -> dict:
 
 
 @dataclass(frozen=True)
+class ColdPageAAD:
+    """Associated data bound to a cold page's tag: the header fields (spec:83-161).
+
+    ``unpack_header`` raises ``ValueError`` on a wrong magic or version and on
+    preset / RoPE-mode nibbles outside the enums, as the reference's does."""
+
+    tenant_id_hash: int
+    model_id_hash: int
+    layer_id: int
+    page_token_hash: int
+    sequence_nonce: int
+    preset: QuantPreset = QuantPreset.K8V4_ASYM
+    rope_mode: RoPEMode = RoPEMode.PRESERVE_FP8
+    head_group_id: int = 0
+
+    @classmethod
+    def from_context(cls, tenant_id: str, model_id: str, layer_id: int, token_ids,
+                     sequence_nonce: int, preset: QuantPreset = QuantPreset.K8V4_ASYM,
+                     rope_mode: RoPEMode = RoPEMode.PRESERVE_FP8) -> "ColdPageAAD":
+        return cls(tenant_id_hash=hash32(tenant_id), model_id_hash=hash32(model_id),
+                   layer_id=layer_id, page_token_hash=hash64_tokens(token_ids),
+                   sequence_nonce=sequence_nonce, preset=preset, rope_mode=rope_mode)
+
+    def pack_header(self) -> bytes:
+        return pack_header(self.preset, self.rope_mode, self.tenant_id_hash, self.model_id_hash,
+                           self.layer_id, self.head_group_id, self.page_token_hash,
+                           self.sequence_nonce)
+
+    @classmethod
+    def unpack_header(cls, header_bytes: bytes) -> "ColdPageAAD":
+        if len(header_bytes) < HEADER_BYTES:
+            raise ValueError(f"Header too short: {len(header_bytes)} < {HEADER_BYTES}")
+        h = unpack_header(header_bytes)
+        if h["magic"] != MAGIC_ZTCP or h["version"] != CODEC_VERSION:
+            raise ValueError(f"Invalid cold-page header magic/version: {hex(h['magic'])} v{h['version']}")
+        return cls(tenant_id_hash=h["tenant_id_hash"], model_id_hash=h["model_id_hash"],
+                   layer_id=h["layer_id"], page_token_hash=h["page_token_hash"],
+                   sequence_nonce=h["sequence_nonce"], preset=QuantPreset(h["preset"]),
+                   rope_mode=RoPEMode(h["rope_mode"] & 0x0F), head_group_id=h["head_group_id"])
+
+
+@dataclass(frozen=True)
 class ColdPageGeometry:
     num_tokens: int = 64
     num_kv_heads: int = 8
@@ -64,6 +106,10 @@ class ColdPageGeometry:
             raise ValueError("head_dim must be a positive multiple of 16")
         if self.rope_dim < 0 or self.rope_dim > self.head_dim or self.rope_dim % 16:
             raise ValueError("Invalid rope_dim")
+
+    @property
+    def nope_dim(self) -> int:
+        return self.head_dim - self.rope_dim
 
     @property
     def vectors_per_buffer(self) -> int:
@@ -98,6 +144,9 @@ class ColdPageGeometry:
 
     def cold_blob_bytes(self, preset: int, rope_mode: int) -> int:
         return HEADER_BYTES + self.payload_bytes(preset, rope_mode) + TAG_BYTES
+
+    def compression_ratio(self, preset: int, rope_mode: int) -> float:
+        return self.hot_page_bytes / self.cold_blob_bytes(preset, rope_mode)
 
 
 def hash32(text: str) -> int:
