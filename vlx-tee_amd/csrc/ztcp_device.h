@@ -157,16 +157,17 @@ __device__ __forceinline__ void chacha_block_cached(const ChaKey& key, const Cha
 // SipHash-2-4 with 128-bit output (cpp:401-471).
 // One page per lane; the chain is strictly sequential, so its cost is the
 // number of VALU issues per 8-byte word.  gfx950 forms used:
-//   * 64-bit add          -> v_lshl_add_u64 (shift 0), one issue;
+//   * 64-bit add          -> v_lshl_add_u64 (shift 0);
 //   * rotate by n < 32    -> two v_alignbit_b32 on the 32-bit halves;
-//   * rotate by 32        -> v_pk_mov_b32 with op_sel, one issue that leaves
-//                            the result in an aligned pair for the next add
-//                            (add-with-carry on exchanged halves costs two
-//                            issues plus a VCC hazard wait);
+//   * rotate by 32        -> never executed: v0's rotation is folded into the
+//                            add that follows it (v_add_co_u32 +
+//                            v_addc_co_u32 on exchanged halves), and v2 is
+//                            kept rotated by 32 between rounds, so the add
+//                            that opens the next round reads it the same way;
 //   * the next word's "v3 ^= m" is folded into the previous round's last
 //     "v3 ^= v0" as a three-input xor (v_bitop3_b32, truth table 0x96).
-// Measured on a lone wave: ~236 shader clocks per word against ~306 for the
-// all-32-bit add/addc formulation.
+// Measured on a lone wave: ~206 shader clocks per word (~212 with an
+// explicit v_pk_mov_b32 exchange for each rotation by 32).
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ uint64_t add_u64(uint64_t a, uint64_t b) {
@@ -174,11 +175,17 @@ __device__ __forceinline__ uint64_t add_u64(uint64_t a, uint64_t b) {
     asm("v_lshl_add_u64 %0, %1, 0, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
-__device__ __forceinline__ uint64_t swap_halves(uint64_t a) {
-    uint64_t r;
-    asm("v_pk_mov_b32 %0, %1, %1 op_sel:[1,0]" : "=v"(r) : "v"(a));
-    return r;
+// rotl(a, 32) + b, with the rotation done by reading a's halves exchanged.
+__device__ __forceinline__ uint64_t add_rot32_u64(uint64_t a, uint64_t b) {
+    uint32_t lo, hi;
+    uint64_t c, c2;
+    asm("v_add_co_u32 %0, %1, %2, %3" : "=v"(lo), "=s"(c) : "v"((uint32_t)(a >> 32)), "v"((uint32_t)b));
+    asm("v_addc_co_u32 %0, %1, %2, %3, %4"
+        : "=v"(hi), "=s"(c2)
+        : "v"((uint32_t)a), "v"((uint32_t)(b >> 32)), "s"(c));
+    return ((uint64_t)hi << 32) | lo;
 }
+__device__ __forceinline__ uint64_t rot32_u64(uint64_t a) { return (a << 32) | (a >> 32); }
 __device__ __forceinline__ uint32_t xor3_u32(uint32_t a, uint32_t b, uint32_t c) {
     uint32_t r;
     asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "v"(c));
@@ -196,12 +203,15 @@ __device__ __forceinline__ uint64_t xor3_u64(uint64_t a, uint64_t b, uint64_t c)
 }
 
 struct Sip {
-    uint64_t v0, v1, v2, v3;
+    // v2r holds rotl(v2, 32): SipRound ends with v2 = rotl(v2, 32), and
+    // keeping it that way lets the next round's "v2 += v3" read the halves
+    // exchanged instead of moving them.
+    uint64_t v0, v1, v2r, v3;
 
     __device__ __forceinline__ void init(uint64_t mk0, uint64_t mk1) {
         v0 = 0x736F6D6570736575ull ^ mk0;
         v1 = 0x646F72616E646F6Dull ^ mk1 ^ 0xEEull;
-        v2 = 0x6C7967656E657261ull ^ mk0;
+        v2r = rot32_u64(0x6C7967656E657261ull ^ mk0);
         v3 = 0x7465646279746573ull ^ mk1;
     }
     // SipRound (cpp:401-416); with INJ the final v3 also takes "^ next", the
@@ -209,15 +219,14 @@ struct Sip {
     template <bool INJ>
     __device__ __forceinline__ void round_(uint64_t next) {
         v0 = add_u64(v0, v1);
-        v2 = add_u64(v2, v3);
+        uint64_t v2 = add_rot32_u64(v2r, v3);  // v2 += v3
         v1 = rotl_u64(v1, 13) ^ v0;
         v3 = rotl_u64(v3, 16) ^ v2;
-        v0 = swap_halves(v0);
-        v0 = add_u64(v0, v3);
+        v0 = add_rot32_u64(v0, v3);            // v0 = rotl(v0, 32) + v3
         v2 = add_u64(v2, v1);
         v3 = INJ ? xor3_u64(rotl_u64(v3, 21), v0, next) : (rotl_u64(v3, 21) ^ v0);
         v1 = rotl_u64(v1, 17) ^ v2;
-        v2 = swap_halves(v2);
+        v2r = v2;                              // v2 = rotl(v2, 32), held rotated
     }
     __device__ __forceinline__ void round() { round_<false>(0); }
     // Compression of one word whose "v3 ^= m" was already applied; the next
@@ -264,12 +273,12 @@ struct Sip {
     // the 128-bit finalization (cpp:447-456).
     __device__ __forceinline__ void finish(uint64_t last_word, uint64_t& lo, uint64_t& hi) {
         absorb(last_word);
-        v2 ^= 0xEEull;
+        v2r ^= 0xEEull << 32;  // v2 ^= 0xee
         round(); round(); round(); round();
-        lo = v0 ^ v1 ^ v2 ^ v3;
+        lo = v0 ^ v1 ^ rot32_u64(v2r) ^ v3;
         v1 ^= 0xDDull;
         round(); round(); round(); round();
-        hi = v0 ^ v1 ^ v2 ^ v3;
+        hi = v0 ^ v1 ^ rot32_u64(v2r) ^ v3;
     }
 };
 
@@ -371,10 +380,13 @@ struct GroupCodes {
     uint32_t scale;           // fp16 scale bits
 };
 
-// Exact emulation of the reference for one group; words by value so the
-// fast path's registers never have to be spilled for this rare call.
+// Exact emulation of the reference for one group.  Inlined (in a cold block
+// at each use): a call would make the caller save registers to scratch
+// around it, and scratch reloads count as memory operations in flight where
+// the rare path joins the fast one, which makes the compiler wait for every
+// outstanding load and store there.
 template <int DT, int BITS>
-__device__ __noinline__ GroupCodes quant_group_exact(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+__device__ __forceinline__ GroupCodes quant_group_exact(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                                      uint32_t w4, uint32_t w5, uint32_t w6, uint32_t w7) {
     const uint32_t w[8] = {w0, w1, w2, w3, w4, w5, w6, w7};
     float amax = 1e-6f;
@@ -445,9 +457,11 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint3
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
-// One group: CW code words (4 for int8, 2 for int4); returns the fp16 scale bits.
+// One group: code words (4 for int8, 2 for int4, the rest zero) and the fp16
+// scale bits, returned by value from both paths so that the caller's
+// registers never go through memory.
 template <int DT, int BITS>
-__device__ __forceinline__ uint32_t quant_group(const uint32_t w[8], uint32_t q[4]) {
+__device__ __forceinline__ GroupCodes quant_group_codes(const uint32_t w[8]) {
     float f[16];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -466,28 +480,39 @@ __device__ __forceinline__ uint32_t quant_group(const uint32_t w[8], uint32_t q[
     const uint32_t sb = scale_fast<BITS>(amax);
     // exact path: NaN / inf elements (amax not < inf), scale zero / subnormal / inf
     const bool special = !(amax < __builtin_inff()) || (sb - 0x0400u) >= (0x7C00u - 0x0400u);
-    if (__builtin_expect(special, 0)) {
-        const GroupCodes r = quant_group_exact<DT, BITS>(w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]);
-        q[0] = r.q0; q[1] = r.q1; q[2] = r.q2; q[3] = r.q3;
-        return r.scale;
-    }
+    if (__builtin_expect(special, 0))
+        return quant_group_exact<DT, BITS>(w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]);
     const float inv = recip_fast(f16_to_f32(sb));
+    GroupCodes r;
+    r.scale = sb;
     if constexpr (BITS == 8) {
         uint32_t t[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) t[i] = __float_as_uint(f[i] * inv + 12582912.0f);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = pack_low_bytes(t[4 * j], t[4 * j + 1], t[4 * j + 2], t[4 * j + 3]);
+        r.q0 = pack_low_bytes(t[0], t[1], t[2], t[3]);
+        r.q1 = pack_low_bytes(t[4], t[5], t[6], t[7]);
+        r.q2 = pack_low_bytes(t[8], t[9], t[10], t[11]);
+        r.q3 = pack_low_bytes(t[12], t[13], t[14], t[15]);
     } else {
         uint32_t b[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)  // bits 0..3 of each sum hold q + 8; bits 4..7 are zero
             b[i] = (__float_as_uint(f[2 * i + 1] * inv + 12582920.0f) << 4) |
                    __float_as_uint(f[2 * i] * inv + 12582920.0f);
-        q[0] = pack_low_bytes(b[0], b[1], b[2], b[3]);
-        q[1] = pack_low_bytes(b[4], b[5], b[6], b[7]);
+        r.q0 = pack_low_bytes(b[0], b[1], b[2], b[3]);
+        r.q1 = pack_low_bytes(b[4], b[5], b[6], b[7]);
+        r.q2 = 0u;
+        r.q3 = 0u;
     }
-    return sb;
+    return r;
+}
+
+// Array form: q[0..3] (int4 fills q[0], q[1]); returns the fp16 scale bits.
+template <int DT, int BITS>
+__device__ __forceinline__ uint32_t quant_group(const uint32_t w[8], uint32_t q[4]) {
+    const GroupCodes r = quant_group_codes<DT, BITS>(w);
+    q[0] = r.q0; q[1] = r.q1; q[2] = r.q2; q[3] = r.q3;
+    return r.scale;
 }
 
 template <int DT>

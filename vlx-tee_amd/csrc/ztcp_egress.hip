@@ -42,20 +42,21 @@ namespace ztcp {
 
 namespace {
 
-constexpr int kRing = 24;             // code rows between producers and the MAC wave
+constexpr int kRing = 30;             // payload rows between their makers and the MAC wave
 constexpr int kStage = 8;             // units whose scales are staged at once
 constexpr int kLdsStage = kRing * kRowWords;
-constexpr int kScaleSlots = 64;      // scale rows the MAC wave may still be waiting for
+constexpr int kScaleSlots = 64;       // scale rows the feeder wave may still be waiting for
 constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
-constexpr int kFlagRing = 0;                          // [kRing] code row index + 1
+constexpr int kFlagRing = 0;                          // [kRing] MAC row index + 1
 constexpr int kFlagStage = kFlagRing + kRing;         // [kStage] unit + 1: staging slot free
 constexpr int kFlagCount = kFlagStage + kStage;       // [kStage] code rows staged in the slot
 constexpr int kFlagScale = kFlagCount + kStage;       // [kScaleSlots] unit + 1: scale row stored
-constexpr int kFlagMacUsed = kFlagScale + kScaleSlots;  // code rows absorbed by the MAC wave
+constexpr int kFlagMacUsed = kFlagScale + kScaleSlots;  // rows absorbed by the MAC wave
 constexpr int kFlagTask = kFlagMacUsed + 1;           // next code row to hand out
-constexpr int kNumFlags = kFlagMacUsed + 4;
+constexpr int kNumFlags = (kFlagTask + 2) & ~1;  // even: the blob table after it is 8-byte aligned
 constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byte aligned)
 constexpr int kLdsWords = kLdsBlobs + 2 * 64;
+static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
 static_assert(kLdsBlobs % 2 == 0, "blob table must be 8-byte aligned");
 
 struct Row {
@@ -64,6 +65,7 @@ struct Row {
     int32_t u, j;     // unit in section, code block in unit
     int32_t g;        // unit index among the page's quantized units (staging slot order)
     int32_t cidx;     // code row index = production order
+    int32_t mrow;     // row index in the MAC wave's order (code rows and scale rows)
     int32_t block;    // payload block index (keystream counter - 1)
     SecRows s;
 };
@@ -87,6 +89,7 @@ __device__ __forceinline__ Row row_info(const Layout& lay, int32_t t) {
             row.scale = s.kind != kSecRaw && row.j == s.nblk - 1;
             row.g = s.qunit_begin + row.u;
             row.cidx = t;
+            row.mrow = t + qb;  // the scale rows of earlier sections come first
             row.block = (int32_t)(s.q_off / 64u) + local;
             row.s = s;
         }
@@ -132,22 +135,6 @@ __device__ __forceinline__ void load_half(const EgressParams& p, const EgressPag
     }
 }
 
-// Stores one row slot to the blobs: lane l writes quad (l & 3) of page
-// 16 k + (l >> 2), so each store instruction writes 64 contiguous bytes of 16
-// pages.  The blob pointers come from the workgroup's LDS table (null past
-// the last page).
-__device__ __forceinline__ void store_row(const uint32_t* slot, const uint32_t* lds, uint32_t blob_off,
-                                          int lane) {
-    const uint64_t* blobs = reinterpret_cast<const uint64_t*>(lds + kLdsBlobs);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int pr = 16 * k + (lane >> 2), q = lane & 3;
-        const uint4 x = lds_quad(slot, pr, q);
-        uint8_t* b = reinterpret_cast<uint8_t*>(blobs[pr]);
-        if (b) stg16(b + blob_off, q, x);
-    }
-}
-
 struct ProducerCtx {
     const EgressParams* p;
     EgressPage pg;
@@ -155,7 +142,61 @@ struct ProducerCtx {
     ChaChaNonceCache nc;
     uint32_t* lds;
     int lane;
+    // Transposed row stores: store k of a row writes quad (lane & 3) of page
+    // 16 k + (lane >> 2).  Past the last page of a partial workgroup the lane
+    // writes page 0's quad instead, the same bytes page 0's own lane writes,
+    // so every store is unconditional (a store under a branch makes the
+    // compiler wait for all outstanding stores before the next row's loads).
+    uint8_t* sb[4];   // blob of the page stored by store k
+    uint32_t sq[4];   // byte offset of that page's quad inside a row slot
+
+    __device__ __forceinline__ void init_stores(int ppw) {
+        const uint64_t* blobs = reinterpret_cast<const uint64_t*>(lds + kLdsBlobs);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int pr = 16 * k + (lane >> 2);
+            const int pe = pr < ppw ? pr : 0;
+            sb[k] = reinterpret_cast<uint8_t*>(blobs[pe]);
+            sq[k] = quad_word(pe, lane & 3) * 4u;
+        }
+    }
 };
+
+// Stores one row slot to the blobs, each store instruction writing 64
+// contiguous bytes of 16 pages.  The four quads are read first, so the row
+// costs one LDS round trip.
+__device__ __forceinline__ void store_row(const uint32_t* slot, const ProducerCtx& c, uint32_t blob_off) {
+    uint4 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = lds_quad_at(slot, c.sq[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) stg16(c.sb[k] + blob_off, c.lane & 3, x[k]);
+}
+
+// A row read back from its slot (transposed, as store_row writes it) whose
+// global stores are issued one row later: the stores then go out after the
+// wave's wait for its next row's groups instead of just before it, so the
+// wave never waits for its own fresh stores (vector memory operations
+// complete in issue order).
+struct HeldRow {
+    uint4 x[4];
+    uint32_t off;   // blob offset of the row
+    int32_t live;   // 0 before the first row
+};
+
+__device__ __forceinline__ void hold_row(const uint32_t* slot, const ProducerCtx& c, uint32_t blob_off, HeldRow& h) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h.x[k] = lds_quad_at(slot, c.sq[k]);
+    h.off = blob_off;
+    h.live = 1;
+}
+
+__device__ __forceinline__ void store_held(const ProducerCtx& c, const HeldRow& h) {
+    if (h.live) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) stg16(c.sb[k] + h.off, c.lane & 3, h.x[k]);
+    }
+}
 
 // Quantizes groups w[0..3] (int8: 4 code words each, int4: 2) into pt[] and
 // their fp16 scales into sc[] (two per word, low half first).
@@ -176,65 +217,17 @@ __device__ __forceinline__ void quant_half(const uint32_t (&w)[4][8], uint32_t* 
     }
 }
 
-// One code row.  w holds the row's first four groups (loaded a row ahead);
-// an int4 row loads its second four during the first half of the keystream.
-// The next row's first groups are loaded as soon as w is free.
-template <int DT, int KIND>
-__device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt, bool prefetch,
-                                         uint32_t (&w)[4][8]) {
-    constexpr int SW = KIND == kSecInt8 ? 2 : (KIND == kSecInt4 ? 4 : 0);  // scale words per row
-    const EgressParams& p = *c.p;
-    uint32_t* flags = c.lds + kLdsFlags;
-    uint32_t pt[16];
-    uint32_t sc[4];
-    ChaChaState st;
-    st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
-    if constexpr (KIND == kSecRaw) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            pt[t] = w[0][t];
-            pt[8 + t] = w[1][t];
-        }
-        if (prefetch) load_half(p, c.pg, nxt, 0, w);
-        st.double_rounds<9>();
-    } else if constexpr (KIND == kSecInt8) {
-        quant_half<DT, 8>(w, pt, sc);
-        if (prefetch) load_half(p, c.pg, nxt, 0, w);
-        st.double_rounds<9>();
-    } else {
-        quant_half<DT, 4>(w, pt, sc);
-        load_half(p, c.pg, row, 1, w);
-        st.double_rounds<4>();
-        quant_half<DT, 4>(w, pt + 8, sc + 2);
-        if (prefetch) load_half(p, c.pg, nxt, 0, w);
-        st.double_rounds<5>();
-    }
-    if constexpr (SW > 0) {
-        // the unit's staging slot is free once unit g - kStage's scale row is done
-        uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
-        wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
-#pragma unroll
-        for (int t = 0; t < SW; ++t) {
-            const int wd = row.j * SW + t;  // logical scale word of this lane's page
-            stage[quad_word(c.lane, wd >> 2) + (wd & 3)] = sc[t];
-        }
-    }
-    uint32_t ks[16];
-    st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
-    uint32_t* slot = c.lds + (row.cidx % kRing) * kRowWords;
-    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.cidx - kRing + 1, p.state);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        lds_put_quad(slot, c.lane, q,
-                     make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
-                                pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
-    store_row(slot, c.lds, (uint32_t)kHeader + 64u * (uint32_t)row.block, c.lane);
-    publish(&flags[kFlagRing + row.cidx % kRing], (uint32_t)row.cidx + 1u);
+// Publishes that scale row g is in the blobs, for the MAC wave to read.
+__device__ __forceinline__ void publish_scale(uint32_t* flags, int32_t g) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    publish(&flags[kFlagScale + g % kScaleSlots], (uint32_t)g + 1u);
 }
 
 // The scale row of row.u's unit, run by the wave that staged the unit's last
-// scales: encrypts the staged scales in place and stores the block.  Frees
-// the staging slot at once; the stores' completion is published later
+// scales, during its next code row (after that row's groups have arrived):
+// encrypts the staged scales in place and stores the block.  Frees the
+// staging slot at once; the stores' completion is published later
 // (publish_scale) so that the wave does not wait for them here.
 __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) {
     const EgressParams& p = *c.p;
@@ -249,16 +242,79 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) 
         lds_put_quad(stage, c.lane, q,
                      make_uint4(s.x ^ ks[4 * q], s.y ^ ks[4 * q + 1], s.z ^ ks[4 * q + 2], s.w ^ ks[4 * q + 3]));
     }
-    store_row(stage, c.lds, (uint32_t)kHeader + 64u * block, c.lane);
+    store_row(stage, c, (uint32_t)kHeader + 64u * block);
     flags[kFlagCount + row.g % kStage] = 0u;
     publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
 }
 
-// Publishes that scale row g is in the blobs, for the MAC wave to read.
-__device__ __forceinline__ void publish_scale(uint32_t* flags, int32_t g) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    publish(&flags[kFlagScale + g % kScaleSlots], (uint32_t)g + 1u);
+// Issues the hot loads of a whole code row: its first four groups into w and,
+// for an int4 row, its second four into w2.
+__device__ __forceinline__ void load_row(const EgressParams& p, const EgressPage& pg, const Row& row,
+                                         uint32_t (&w)[4][8], uint32_t (&w2)[4][8]) {
+    load_half(p, pg, row, 0, w);
+    if (row.s.kind == kSecInt4) load_half(p, pg, row, 1, w2);
+}
+
+// One code row.  w (and w2 for int4) hold the row's groups, loaded a row
+// ahead.  Every kind of row issues the next row's loads at the same point
+// (after its groups are quantized, with half of the keystream still to do),
+// into the same registers, so that no path has to move a register whose
+// load is still in flight -- such a move would make the wave wait for it.
+template <int DT>
+__device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt,
+                                         uint32_t (&w)[4][8], uint32_t (&w2)[4][8], HeldRow& held,
+                                         const Row& unit_done, bool make_scale) {
+    const EgressParams& p = *c.p;
+    uint32_t* flags = c.lds + kLdsFlags;
+    const int32_t kind = row.s.kind;
+    uint32_t pt[16];
+    uint32_t sc[4];
+    ChaChaState st;
+    st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
+    if (kind == kSecInt8) {
+        quant_half<DT, 8>(w, pt, sc);
+    } else if (kind == kSecInt4) {
+        quant_half<DT, 4>(w, pt, sc);
+        quant_half<DT, 4>(w2, pt + 8, sc + 2);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            pt[t] = w[0][t];
+            pt[8 + t] = w[1][t];
+        }
+    }
+    store_held(c, held);  // the previous row's stores, after this row's groups have arrived
+    if (make_scale) scale_row(c, unit_done);
+    st.double_rounds<4>();
+    if (nxt.valid) load_row(p, c.pg, nxt, w, w2);
+    st.double_rounds<5>();
+    if (kind != kSecRaw) {
+        // the unit's staging slot is free once unit g - kStage's scale row is done
+        uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
+        wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
+        const int sw = kind == kSecInt8 ? 2 : 4;  // scale words of this row
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (t < sw) {
+                const int wd = row.j * sw + t;  // logical scale word of this lane's page
+                stage[quad_word(c.lane, wd >> 2) + (wd & 3)] = sc[t];
+            }
+        }
+    }
+    uint32_t ks[16];
+    st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
+    // the scale row made above is published before this row's only wait
+    // that depends on the MAC wave (which may be waiting for that scale row)
+    if (make_scale) publish_scale(flags, unit_done.g);
+    uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
+    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, p.state);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        lds_put_quad(slot, c.lane, q,
+                     make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
+                                pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
+    hold_row(slot, c, (uint32_t)kHeader + 64u * (uint32_t)row.block, held);
+    publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);
 }
 
 template <int DT>
@@ -272,7 +328,13 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     c.n2 = c.pg.nonce2;
     c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
+    c.init_stores(ppw);
     const int32_t total = total_code_rows(p.lay);
+    // The page descriptor and kernel argument loads above complete here,
+    // before the loop: a load still counted as in flight where the loop
+    // begins makes the compiler wait for every outstanding memory operation
+    // wherever the loop uses its result.
+    __builtin_amdgcn_s_waitcnt(0);
     uint32_t* flags = lds + kLdsFlags;
     // code rows are handed out in order from an LDS counter, one row ahead of
     // the one being made (so its groups can be prefetched): a slower wave
@@ -283,83 +345,106 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
             t = __hip_atomic_fetch_add(&flags[kFlagTask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         return (int32_t)__builtin_amdgcn_readfirstlane(t);
     };
-    uint32_t w[4][8];
+    uint32_t w[4][8], w2[4][8];
+    HeldRow held;
+    held.live = 0;
+    Row unit_done{};         // unit whose last code row this wave staged
+    bool make_scale = false;  // its scale row is still to be made
     int32_t t = grab();
     Row cur = row_info(p.lay, t);
-    if (cur.valid) load_half(p, c.pg, cur, 0, w);
-    int32_t pending = -1;  // scale row whose store completion is not yet published
+    if (cur.valid) load_row(p, c.pg, cur, w, w2);
 #pragma unroll 1
     while (t < total) {
-        if (pending >= 0) {  // the wave waits for this row's prefetched groups here anyway
-            publish_scale(flags, pending);
-            pending = -1;
-        }
         const int32_t tn = grab();
         const Row nxt = row_info(p.lay, tn);
-        if (cur.s.kind == kSecInt8)
-            code_row<DT, kSecInt8>(c, cur, nxt, nxt.valid, w);
-        else if (cur.s.kind == kSecInt4)
-            code_row<DT, kSecInt4>(c, cur, nxt, nxt.valid, w);
-        else
-            code_row<DT, kSecRaw>(c, cur, nxt, nxt.valid, w);
+        code_row<DT>(c, cur, nxt, w, w2, held, unit_done, make_scale);
+        make_scale = false;
         if (cur.s.kind != kSecRaw) {
             // count the unit's staged code rows; whoever stages the last one
-            // encrypts the unit's scales
+            // encrypts the unit's scales (during its next row)
             uint32_t old = 0;
             if (c.lane == 0)
                 old = __hip_atomic_fetch_add(&flags[kFlagCount + cur.g % kStage], 1u, __ATOMIC_ACQ_REL,
                                              __HIP_MEMORY_SCOPE_WORKGROUP);
             old = __builtin_amdgcn_readfirstlane(old);
             if (old == (uint32_t)cur.s.nblk - 1u) {
-                scale_row(c, cur);
-                pending = cur.g;
+                unit_done = cur;
+                make_scale = true;
             }
         }
         t = tn;
         cur = nxt;
     }
-    if (pending >= 0) publish_scale(flags, pending);
+    if (make_scale) scale_row(c, unit_done);
+    store_held(c, held);
+    if (make_scale) publish_scale(flags, unit_done.g);
 }
 
-// The MAC wave's view of the payload: each section's code rows (LDS ring),
-// then its scale rows (blobs).
-struct MacFeed {
-    int32_t si, phase, i;
-    int32_t cidx;
-    int32_t code_begin, qunit_begin;
+// Section sizes of the page layout in scalar registers: code rows and scale
+// rows per section, and the payload offset of each section's scales.  The
+// values pass through an empty asm so that the compiler keeps them in
+// registers instead of reloading them from the kernel arguments inside the
+// MAC loop (a scalar load there would make the wave wait for its LDS reads).
+struct MacPlan {
+    int32_t nc0, nc1, nc2;     // code rows per section
+    int32_t ns0, ns1, ns2;     // scale rows per section (0 for raw sections)
+    uint32_t so0, so1, so2;    // payload offset of the section's scales
+    int32_t total;             // rows absorbed after the header
 
-    __device__ __forceinline__ void fetch(const EgressParams& p, const uint8_t* pay, const uint32_t* lds,
-                                          int lane, uint4 (&x)[4], int32_t& tag) {
-        const uint32_t* flags = lds + kLdsFlags;
-        const SecRows s = sec_rows(p.lay, si, code_begin, qunit_begin);
-        if (phase == 0) {
-            const uint32_t* slot = lds + (cidx % kRing) * kRowWords;
-            wait_ge<kDiagEgressWait>(&flags[kFlagRing + cidx % kRing], cidx + 1, p.state);
+    __device__ __forceinline__ void init(const Layout& lay) {
+        int32_t nc[3], ns[3];
+        uint32_t so[3];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) x[q] = lds_quad(slot, lane, q);
-            tag = cidx + 1;
-            ++cidx;
-            if (++i == s.n_units * s.nblk) {
-                i = 0;
-                phase = s.kind != kSecRaw ? 1 : 2;
-            }
-        } else {
-            const int32_t g = s.qunit_begin + i;
-            wait_ge<kDiagEgressWait>(&flags[kFlagScale + g % kScaleSlots], g + 1, p.state);
-            const uint8_t* q = pay + s.s_off + 64u * (uint32_t)i;
-            x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
-            tag = 0;
-            if (++i == s.n_units) phase = 2;
+        for (int si = 0; si < 3; ++si) {
+            const bool on = si < lay.n_sec;
+            const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
+            const int32_t nu = ZTCP_SEC_FIELD(lay, si, n_units);
+            nc[si] = on ? nu * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16)) : 0;
+            ns[si] = on && kind != kSecRaw ? nu : 0;
+            so[si] = ZTCP_SEC_FIELD(lay, si, s_off);
         }
-        if (phase == 2) {  // next section
-            code_begin += s.n_units * s.nblk;
-            if (s.kind != kSecRaw) qunit_begin += s.n_units;
-            ++si;
-            phase = 0;
-            i = 0;
-        }
+        nc0 = nc[0]; nc1 = nc[1]; nc2 = nc[2];
+        ns0 = ns[0]; ns1 = ns[1]; ns2 = ns[2];
+        so0 = so[0]; so1 = so[1]; so2 = so[2];
+        asm volatile("" : "+s"(nc0), "+s"(nc1), "+s"(nc2), "+s"(ns0), "+s"(ns1), "+s"(ns2));
+        asm volatile("" : "+s"(so0), "+s"(so1), "+s"(so2));
+        total = nc0 + nc1 + nc2 + ns0 + ns1 + ns2;
     }
+    __device__ __forceinline__ int32_t nc(int32_t si) const { return si == 0 ? nc0 : (si == 1 ? nc1 : (si == 2 ? nc2 : 0)); }
+    __device__ __forceinline__ int32_t ns(int32_t si) const { return si == 0 ? ns0 : (si == 1 ? ns1 : (si == 2 ? ns2 : 0)); }
 };
+
+// One fetched row: its 64 bytes for this lane's page and the value of the
+// row's ready flag, read just before the data.  LDS operations of a wave are
+// performed in order, and a row's maker writes it before it releases the
+// row's flag; so when the flag read shows the row, the data read after it
+// holds the row.  Otherwise the row is read again once the flag is set.
+struct MacRow {
+    uint4 x[4];
+    uint32_t f;
+    int32_t slot;  // ring slot (wave-uniform)
+};
+
+__device__ __forceinline__ void mac_fetch(const uint32_t* lds, const PageQuads& pq, int32_t slot, MacRow& r) {
+    r.slot = slot;
+    r.f = __hip_atomic_load(lds + kLdsFlags + kFlagRing + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");  // the data reads stay after the flag read
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(lds + slot * kRowWords, pq.off[q]);
+}
+
+// Absorbs MAC row `want - 1` (re-reading it if it was not ready when
+// fetched) and releases its slot.
+__device__ __forceinline__ void mac_absorb(DeviceState* st, uint32_t* lds, const PageQuads& pq, Sip& s,
+                                           MacRow& r, int32_t want) {
+    if ((int32_t)__builtin_amdgcn_readfirstlane(r.f) < want) {
+        wait_ge<kDiagEgressWait>(lds + kLdsFlags + kFlagRing + r.slot, want, st);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(lds + r.slot * kRowWords, pq.off[q]);
+    }
+    s.absorb64(r.x);
+    publish(lds + kLdsFlags + kFlagMacUsed, (uint32_t)want);
+}
 
 template <int DT>
 __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
@@ -377,35 +462,104 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     s.init(p.mk0, p.mk1);
     const uint64_t hdr[4] = {p.hdr0, pg.hdr1, pg.token, pg.seq};
     s.absorb_words<4>(hdr);
-    const uint8_t* pay = blob + kHeader;
-    uint32_t* used = lds + kLdsFlags + kFlagMacUsed;
-    MacFeed feed{0, 0, 0, 0, 0, 0};
-    const int32_t total = total_rows(p.lay);
-    // three chunks in flight: two fetched ahead of the one being absorbed; a
-    // code row's ring slot is released once it has been absorbed
-    uint4 x0[4], x1[4], x2[4];
-    int32_t t0 = 0, t1 = 0, t2 = 0;
-    if (total > 0) feed.fetch(p, pay, lds, lane, x0, t0);
-    if (total > 1) feed.fetch(p, pay, lds, lane, x1, t1);
+    PageQuads pq;
+    pq.init(lane);
+    MacPlan m;
+    m.init(p.lay);
+    const int32_t total = m.total;
+    // Rows arrive in MAC order in the ring (code rows from the producers,
+    // scale rows from the feeder), so the next row is always the next slot.
+    // Two rows are in flight; a row is fetched right after the absorption
+    // that frees its registers, so every read has a whole row's absorption
+    // to complete before it is used and no wait lands on a fresh read.
+    // Fetches are unconditional (past the last row they read slots that are
+    // never absorbed): a fetch under a branch would leave the buffer in
+    // different registers on the two paths, and the copy that joins them
+    // would wait for the fresh read.
+    // Every load issued so far completes before the loop: a load still
+    // counted as in flight where the loop begins (a scalar load in
+    // particular, as those complete out of order) would turn the loop's LDS
+    // waits into full waits.
+    DeviceState* st = p.state;
+    __builtin_amdgcn_s_waitcnt(0);
+    MacRow r0, r1;
+    int32_t slot = 0;
+    auto next_slot = [&]() { const int32_t v = slot; slot = slot == kRing - 1 ? 0 : slot + 1; return v; };
+    mac_fetch(lds, pq, next_slot(), r0);
+    mac_fetch(lds, pq, next_slot(), r1);
 #pragma unroll 1
-    for (int32_t c = 0; c < total; c += 3) {
-        if (c + 2 < total) feed.fetch(p, pay, lds, lane, x2, t2);
-        s.absorb64(x0);
-        if (t0) publish(used, (uint32_t)t0);
+    for (int32_t c = 0; c < total; c += 2) {
+        mac_absorb(st, lds, pq, s, r0, c + 1);
+        mac_fetch(lds, pq, next_slot(), r0);
         if (c + 1 >= total) break;
-        if (c + 3 < total) feed.fetch(p, pay, lds, lane, x0, t0);
-        s.absorb64(x1);
-        if (t1) publish(used, (uint32_t)t1);
-        if (c + 2 >= total) break;
-        if (c + 4 < total) feed.fetch(p, pay, lds, lane, x1, t1);
-        s.absorb64(x2);
-        if (t2) publish(used, (uint32_t)t2);
+        mac_absorb(st, lds, pq, s, r1, c + 2);
+        mac_fetch(lds, pq, next_slot(), r1);
     }
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     if (active)
         stg16(blob + kHeader + p.payload, 0,
               make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)));
+}
+
+// Scale-row feeder (a wave on the MAC wave's SIMD, almost idle): copies each
+// section's encrypted scale rows from the blobs into the ring, at their place
+// in the MAC wave's order, where the MAC wave reads them like code rows.  A scale row is stored long
+// before the MAC wave reaches it (after all of its section's code rows), so
+// it is no longer in L2; the feeder takes that latency instead of the MAC
+// chain.  Within a section the next row's loads are in flight while the
+// current one is written; a section's first row is never waited for before
+// the previous section's rows are all in the ring, so the MAC wave never
+// depends on a row that needs it to progress first.
+__device__ __forceinline__ void feed_load(const EgressParams& p, const uint32_t* lds, const uint8_t* src,
+                                          int32_t g, uint4 (&x)[4]) {
+    wait_ge<kDiagEgressWait>(lds + kLdsFlags + kFlagScale + g % kScaleSlots, g + 1, p.state);
+    if (src) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[q] = ldg16(src, q);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[q] = make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+__device__ __forceinline__ void feed_put(const EgressParams& p, uint32_t* lds, const PageQuads& pq, int32_t rs,
+                                         const uint4 (&x)[4]) {
+    uint32_t* flags = lds + kLdsFlags;
+    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], rs - kRing + 1, p.state);
+    uint32_t* slot = lds + (rs % kRing) * kRowWords;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
+    publish(&flags[kFlagRing + rs % kRing], (uint32_t)rs + 1u);
+}
+
+__device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
+    const int lane = threadIdx.x & 63;
+    const uint8_t* blob = reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint64_t*>(lds + kLdsBlobs)[lane]);
+    PageQuads pq;
+    pq.init(lane);
+    MacPlan m;
+    m.init(p.lay);
+    int32_t g0 = 0, r0 = 0;  // scale rows / MAC rows before the section
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        const int32_t n = m.ns(si);
+        const int32_t rs = r0 + m.nc(si);  // MAC row of the section's first scale row
+        const uint32_t so = si == 0 ? m.so0 : (si == 1 ? m.so1 : m.so2);
+        const uint8_t* base = blob ? blob + kHeader + so : nullptr;
+        uint4 a[4], b[4];
+        if (n > 0) feed_load(p, lds, base, g0, a);
+#pragma unroll 1
+        for (int32_t j = 0; j < n; j += 2) {
+            if (j + 1 < n) feed_load(p, lds, base ? base + 64u * (uint32_t)(j + 1) : nullptr, g0 + j + 1, b);
+            feed_put(p, lds, pq, rs + j, a);
+            if (j + 1 >= n) break;
+            if (j + 2 < n) feed_load(p, lds, base ? base + 64u * (uint32_t)(j + 2) : nullptr, g0 + j + 2, a);
+            feed_put(p, lds, pq, rs + j + 1, b);
+        }
+        g0 += n;
+        r0 = rs + n;
+    }
 }
 
 template <int DT>
@@ -417,13 +571,17 @@ __global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParam
     if (threadIdx.x < 64) {
         uint64_t* blobs = reinterpret_cast<uint64_t*>(lds + kLdsBlobs);
         blobs[threadIdx.x] = (int)threadIdx.x < ppw ? reinterpret_cast<uint64_t>(egress_page(p, page0 + threadIdx.x).blob)
-                                                    : 0ull;  // no stores past the last page
+                                                    : 0ull;  // null past the last page
     }
     __syncthreads();
     const int wave = threadIdx.x >> 6;
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
         egress_mac<DT>(p, page0, ppw, lds);
+        return;
+    }
+    if (wave == 4) {
+        egress_scale_feed(p, lds);
         return;
     }
     if ((wave & 3) == 0) return;  // leave the MAC wave's SIMD to it

@@ -23,7 +23,8 @@ __device__ __forceinline__ uint32_t quad_word(int pg, int q) {
 }
 
 __device__ __forceinline__ uint4 lds_quad(const uint32_t* row, int pg, int q) {
-    return *reinterpret_cast<const uint4*>(row + quad_word(pg, q));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(row + quad_word(pg, q));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ void lds_put_quad(uint32_t* row, int pg, int q, uint4 x) {
     *reinterpret_cast<uint4*>(row + quad_word(pg, q)) = x;
@@ -39,8 +40,11 @@ struct PageQuads {
     }
 };
 
+// Loaded as a 4 x u32 vector: reading a uint4 struct lets the compiler turn
+// the 64-bit word views of the quad into a second, overlapping LDS read.
 __device__ __forceinline__ uint4 lds_quad_at(const uint32_t* row, uint32_t byte_off) {
-    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(row) + byte_off);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(row) + byte_off);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ void lds_put_quad_at(uint32_t* row, uint32_t byte_off, uint4 x) {
     *reinterpret_cast<uint4*>(reinterpret_cast<char*>(row) + byte_off) = x;
