@@ -42,6 +42,12 @@ namespace ztcp {
 
 namespace {
 
+// 16 waves, four per SIMD: the MAC wave (0) and the scale-row feeder (4) on
+// SIMD 0 (waves 8 and 12 exit at once: producers there slow the MAC chain
+// down more than they add), twelve producers on the other three SIMDs.
+// 128 VGPRs each.
+constexpr int kEgressWaves = 16;
+constexpr int kEgressThreads = 64 * kEgressWaves;
 constexpr int kRing = 30;             // payload rows between their makers and the MAC wave
 constexpr int kStage = 8;             // units whose scales are staged at once
 constexpr int kLdsStage = kRing * kRowWords;
@@ -164,38 +170,15 @@ struct ProducerCtx {
 
 // Stores one row slot to the blobs, each store instruction writing 64
 // contiguous bytes of 16 pages.  The four quads are read first, so the row
-// costs one LDS round trip.
+// costs one LDS round trip.  The stores are issued after the next row's
+// loads, so the wave's wait for those loads does not include them (vector
+// memory operations complete in issue order).
 __device__ __forceinline__ void store_row(const uint32_t* slot, const ProducerCtx& c, uint32_t blob_off) {
     uint4 x[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) x[k] = lds_quad_at(slot, c.sq[k]);
 #pragma unroll
     for (int k = 0; k < 4; ++k) stg16(c.sb[k] + blob_off, c.lane & 3, x[k]);
-}
-
-// A row read back from its slot (transposed, as store_row writes it) whose
-// global stores are issued one row later: the stores then go out after the
-// wave's wait for its next row's groups instead of just before it, so the
-// wave never waits for its own fresh stores (vector memory operations
-// complete in issue order).
-struct HeldRow {
-    uint4 x[4];
-    uint32_t off;   // blob offset of the row
-    int32_t live;   // 0 before the first row
-};
-
-__device__ __forceinline__ void hold_row(const uint32_t* slot, const ProducerCtx& c, uint32_t blob_off, HeldRow& h) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) h.x[k] = lds_quad_at(slot, c.sq[k]);
-    h.off = blob_off;
-    h.live = 1;
-}
-
-__device__ __forceinline__ void store_held(const ProducerCtx& c, const HeldRow& h) {
-    if (h.live) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) stg16(c.sb[k] + h.off, c.lane & 3, h.x[k]);
-    }
 }
 
 // Quantizes groups w[0..3] (int8: 4 code words each, int4: 2) into pt[] and
@@ -247,23 +230,18 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) 
     publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
 }
 
-// Issues the hot loads of a whole code row: its first four groups into w and,
-// for an int4 row, its second four into w2.
-__device__ __forceinline__ void load_row(const EgressParams& p, const EgressPage& pg, const Row& row,
-                                         uint32_t (&w)[4][8], uint32_t (&w2)[4][8]) {
-    load_half(p, pg, row, 0, w);
-    if (row.s.kind == kSecInt4) load_half(p, pg, row, 1, w2);
-}
-
-// One code row.  w (and w2 for int4) hold the row's groups, loaded a row
-// ahead.  Every kind of row issues the next row's loads at the same point
-// (after its groups are quantized, with half of the keystream still to do),
-// into the same registers, so that no path has to move a register whose
-// load is still in flight -- such a move would make the wave wait for it.
+// One code row.  w holds the row's first four groups, loaded a row ahead;
+// an int4 row loads its second four into w once the first four are
+// quantized, and uses them after four double rounds.  Every kind of row
+// issues the next row's loads at the same point, into the same registers,
+// so that no path has to move a register whose load is still in flight
+// (such a move would make the wave wait for it).  A scale row this wave owes
+// (the last code row of a unit it staged) is made right after this row's
+// groups have arrived and published before this row's only wait that
+// depends on the MAC wave.
 template <int DT>
 __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt,
-                                         uint32_t (&w)[4][8], uint32_t (&w2)[4][8], HeldRow& held,
-                                         const Row& unit_done, bool make_scale) {
+                                         uint32_t (&w)[4][8], const Row& unit_done, bool make_scale) {
     const EgressParams& p = *c.p;
     uint32_t* flags = c.lds + kLdsFlags;
     const int32_t kind = row.s.kind;
@@ -275,7 +253,6 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         quant_half<DT, 8>(w, pt, sc);
     } else if (kind == kSecInt4) {
         quant_half<DT, 4>(w, pt, sc);
-        quant_half<DT, 4>(w2, pt + 8, sc + 2);
     } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -283,10 +260,11 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
             pt[8 + t] = w[1][t];
         }
     }
-    store_held(c, held);  // the previous row's stores, after this row's groups have arrived
+    if (kind == kSecInt4) load_half(p, c.pg, row, 1, w);
     if (make_scale) scale_row(c, unit_done);
     st.double_rounds<4>();
-    if (nxt.valid) load_row(p, c.pg, nxt, w, w2);
+    if (kind == kSecInt4) quant_half<DT, 4>(w, pt + 8, sc + 2);
+    if (nxt.valid) load_half(p, c.pg, nxt, 0, w);
     st.double_rounds<5>();
     if (kind != kSecRaw) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
@@ -303,8 +281,6 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     }
     uint32_t ks[16];
     st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
-    // the scale row made above is published before this row's only wait
-    // that depends on the MAC wave (which may be waiting for that scale row)
     if (make_scale) publish_scale(flags, unit_done.g);
     uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
     wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, p.state);
@@ -313,7 +289,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         lds_put_quad(slot, c.lane, q,
                      make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
                                 pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
-    hold_row(slot, c, (uint32_t)kHeader + 64u * (uint32_t)row.block, held);
+    store_row(slot, c, (uint32_t)kHeader + 64u * (uint32_t)row.block);
     publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);
 }
 
@@ -345,19 +321,17 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
             t = __hip_atomic_fetch_add(&flags[kFlagTask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         return (int32_t)__builtin_amdgcn_readfirstlane(t);
     };
-    uint32_t w[4][8], w2[4][8];
-    HeldRow held;
-    held.live = 0;
+    uint32_t w[4][8];
     Row unit_done{};         // unit whose last code row this wave staged
     bool make_scale = false;  // its scale row is still to be made
     int32_t t = grab();
     Row cur = row_info(p.lay, t);
-    if (cur.valid) load_row(p, c.pg, cur, w, w2);
+    if (cur.valid) load_half(p, c.pg, cur, 0, w);
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
         const Row nxt = row_info(p.lay, tn);
-        code_row<DT>(c, cur, nxt, w, w2, held, unit_done, make_scale);
+        code_row<DT>(c, cur, nxt, w, unit_done, make_scale);
         make_scale = false;
         if (cur.s.kind != kSecRaw) {
             // count the unit's staged code rows; whoever stages the last one
@@ -375,9 +349,10 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
         t = tn;
         cur = nxt;
     }
-    if (make_scale) scale_row(c, unit_done);
-    store_held(c, held);
-    if (make_scale) publish_scale(flags, unit_done.g);
+    if (make_scale) {
+        scale_row(c, unit_done);
+        publish_scale(flags, unit_done.g);
+    }
 }
 
 // Section sizes of the page layout in scalar registers: code rows and scale
@@ -563,7 +538,7 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParams p) {
+__global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
@@ -584,7 +559,7 @@ __global__ __launch_bounds__(kFusedThreads) void egress_fused_kernel(EgressParam
         egress_scale_feed(p, lds);
         return;
     }
-    if ((wave & 3) == 0) return;  // leave the MAC wave's SIMD to it
+    if ((wave & 3) == 0) return;  // the rest of the MAC wave's SIMD stays idle
     egress_produce<DT>(p, page0, ppw, lds);
 }
 
@@ -596,9 +571,9 @@ hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) 
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     const size_t lds = egress_fused_lds_bytes();  // above 64 KiB: gfx950 has 160 KiB per CU
     if (dtype == kHotBf16)
-        hipLaunchKernelGGL(egress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kFusedThreads), lds, s, p);
+        hipLaunchKernelGGL(egress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kEgressThreads), lds, s, p);
     else
-        hipLaunchKernelGGL(egress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kFusedThreads), lds, s, p);
+        hipLaunchKernelGGL(egress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kEgressThreads), lds, s, p);
     return hipGetLastError();
 }
 
