@@ -117,8 +117,12 @@ def test_roundtrip_matches_oracle(hip, O, geo, dtype):
     assert hip.device_diag() == 0
 
 
-@pytest.mark.parametrize("pad", [4, 68, 132])
-def test_padded_payload_generic_path(hip, O, pad):
+@pytest.mark.parametrize("pad", [4, 16, 48, 68, 80, 128, 132])
+def test_padded_payload(hip, O, pad):
+    """Payload longer than the layout: egress always takes the generic
+    kernels; ingress takes the fused kernel when the blob size is a multiple
+    of 16 (padding rows and a 16/32/48-byte tail on the verify path) and the
+    generic kernels otherwise."""
     T, Hh, D, R, mla, B = 16, 4, 128, 64, False, 5
     k, v = _pages(3, B, T, Hh, D, R, mla, torch.bfloat16)
     th = np.arange(B, dtype=np.int64)

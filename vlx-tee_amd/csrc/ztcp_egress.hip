@@ -389,38 +389,6 @@ struct MacPlan {
     __device__ __forceinline__ int32_t ns(int32_t si) const { return si == 0 ? ns0 : (si == 1 ? ns1 : (si == 2 ? ns2 : 0)); }
 };
 
-// One fetched row: its 64 bytes for this lane's page and the value of the
-// row's ready flag, read just before the data.  LDS operations of a wave are
-// performed in order, and a row's maker writes it before it releases the
-// row's flag; so when the flag read shows the row, the data read after it
-// holds the row.  Otherwise the row is read again once the flag is set.
-struct MacRow {
-    uint4 x[4];
-    uint32_t f;
-    int32_t slot;  // ring slot (wave-uniform)
-};
-
-__device__ __forceinline__ void mac_fetch(const uint32_t* lds, const PageQuads& pq, int32_t slot, MacRow& r) {
-    r.slot = slot;
-    r.f = __hip_atomic_load(lds + kLdsFlags + kFlagRing + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    asm volatile("" ::: "memory");  // the data reads stay after the flag read
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(lds + slot * kRowWords, pq.off[q]);
-}
-
-// Absorbs MAC row `want - 1` (re-reading it if it was not ready when
-// fetched) and releases its slot.
-__device__ __forceinline__ void mac_absorb(DeviceState* st, uint32_t* lds, const PageQuads& pq, Sip& s,
-                                           MacRow& r, int32_t want) {
-    if ((int32_t)__builtin_amdgcn_readfirstlane(r.f) < want) {
-        wait_ge<kDiagEgressWait>(lds + kLdsFlags + kFlagRing + r.slot, want, st);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(lds + r.slot * kRowWords, pq.off[q]);
-    }
-    s.absorb64(r.x);
-    publish(lds + kLdsFlags + kFlagMacUsed, (uint32_t)want);
-}
-
 template <int DT>
 __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
     const int lane = threadIdx.x & 63;
@@ -441,35 +409,12 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     pq.init(lane);
     MacPlan m;
     m.init(p.lay);
-    const int32_t total = m.total;
     // Rows arrive in MAC order in the ring (code rows from the producers,
     // scale rows from the feeder), so the next row is always the next slot.
-    // Two rows are in flight; a row is fetched right after the absorption
-    // that frees its registers, so every read has a whole row's absorption
-    // to complete before it is used and no wait lands on a fresh read.
-    // Fetches are unconditional (past the last row they read slots that are
-    // never absorbed): a fetch under a branch would leave the buffer in
-    // different registers on the two paths, and the copy that joins them
-    // would wait for the fresh read.
-    // Every load issued so far completes before the loop: a load still
-    // counted as in flight where the loop begins (a scalar load in
-    // particular, as those complete out of order) would turn the loop's LDS
-    // waits into full waits.
     DeviceState* st = p.state;
     __builtin_amdgcn_s_waitcnt(0);
-    MacRow r0, r1;
-    int32_t slot = 0;
-    auto next_slot = [&]() { const int32_t v = slot; slot = slot == kRing - 1 ? 0 : slot + 1; return v; };
-    mac_fetch(lds, pq, next_slot(), r0);
-    mac_fetch(lds, pq, next_slot(), r1);
-#pragma unroll 1
-    for (int32_t c = 0; c < total; c += 2) {
-        mac_absorb(st, lds, pq, s, r0, c + 1);
-        mac_fetch(lds, pq, next_slot(), r0);
-        if (c + 1 >= total) break;
-        mac_absorb(st, lds, pq, s, r1, c + 2);
-        mac_fetch(lds, pq, next_slot(), r1);
-    }
+    mac_rows<kRing, kDiagEgressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
+                                     m.total);
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     if (active)

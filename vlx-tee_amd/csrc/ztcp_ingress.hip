@@ -3,36 +3,39 @@
 // HBM read of the blob and one HBM write of the hot page.  Replaces the
 // per-page decoder of fused_decode_cold_pages_peak_into_cpu (cpp:2309-2463).
 //
-// One workgroup handles up to 64 pages with 12 waves (lane = page):
+// One workgroup handles up to 64 pages with 16 waves, four per SIMD (lane =
+// page in every wave):
 //   * Every page is decoded according to its own header flags.  The
 //     workgroup's layout is that of its first page with valid flags; pages
 //     with that layout go through the row pipeline below, pages with another
 //     valid layout are decoded afterwards unit by unit, pages with invalid
 //     flags are not decoded (they fail with status 1).
-//   * Nine decoder waves take rows in order from an LDS counter, each with
-//     its ciphertext block loaded one row ahead.  A unit's scale row is
-//     decrypted into an LDS staging slot two units ahead of its code rows.  A
-//     code row first puts its ciphertext into a ring of row slots in LDS for
-//     the verify wave, then decrypts, takes its scales from staging and
-//     dequantizes two groups at a time into a per-wave LDS tile, from which
-//     the wave stores them transposed: four lanes per page, so each store
-//     writes the two groups (64 bytes, contiguous within a head vector) of
-//     16 pages.
-//   * Wave 0 verifies one page per lane at raised priority on a SIMD of its
-//     own (waves 4 and 8, which the dispatcher places there, exit at once):
+//   * Twelve decoder waves (on SIMDs 1-3) take rows in order from an LDS
+//     counter, each with its ciphertext block loaded one row ahead.  A
+//     unit's scale row is decrypted into an LDS staging slot two units ahead
+//     of its code rows.  A code row first puts its ciphertext into a ring of
+//     row slots in LDS, at its place in payload order, then decrypts, takes
+//     its scales from staging and dequantizes two groups at a time into a
+//     per-wave LDS tile, from which the wave stores them transposed: four
+//     lanes per page, so each store writes the two groups (64 bytes,
+//     contiguous within a head vector) of 16 pages.
+//   * Wave 0 verifies one page per lane at raised priority on SIMD 0:
 //     magic/version (status 1), AAD tenant/model/layer/token hash (status
 //     2), the SipHash-2-4-128 tag over header || ciphertext (status 3), then
 //     flags and payload size (status 1), in the reference's order
-//     (cpp:2313-2355).  Code rows of the workgroup's layout come from the
-//     LDS ring, every other 64-byte chunk (scales, padding) from the blob.
+//     (cpp:2313-2355).  It reads the payload's 64-byte rows in order from the
+//     ring: code rows come from the decoders, every other row (scales,
+//     padding) from a feeder wave (wave 4, on SIMD 0 as well), which copies
+//     them from the blob so that the verify wave's chain never waits for
+//     global memory.  Waves 8 and 12 exit at once.
 //   * Decoding is speculative: a page whose verdict is not OK has its outputs
 //     zeroed before the kernel ends (per-page mode) or by the finalize kernel
 //     (all-or-nothing mode, which zeroes every output, cpp:2481-2486).
 //     Outputs are only valid after the call returns OK, as with the
 //     reference.
-//   * Hand-offs are monotonic LDS counters (ring_flag, mac_used, scale_ready,
-//     scale_free) with workgroup-scope release/acquire; every wait is bounded
-//     and only points backwards in row order.
+//   * Hand-offs are monotonic LDS counters (ring flags, mac_used,
+//     scale_ready, scale_free) with workgroup-scope release/acquire; every
+//     wait is bounded and only points backwards in payload or task order.
 // Requires 16-byte aligned blobs / outputs, blob_bytes % 16 == 0 and every
 // layout aligned to 64-byte units; otherwise the host uses the generic path.
 #include "ztcp_rows.h"
@@ -41,25 +44,31 @@ namespace ztcp {
 
 namespace {
 
-constexpr int kRing = 16;        // code rows between decoders and the verify wave
-constexpr int kStage = 8;        // units whose decrypted scales are staged at once
-constexpr int kLookahead = 2;    // a unit's scale row is handed out this many units early
+constexpr int kIngressWaves = 16;
+constexpr int kIngressThreads = 64 * kIngressWaves;
+constexpr int kDecoderWaves = 12;  // the waves on SIMDs 1-3
+constexpr int kRing = 18;          // payload rows between their makers and the verify wave
+constexpr int kStage = 8;          // units whose decrypted scales are staged at once
+constexpr int kLookahead = 2;      // a unit's scale row is handed out this many units early
 constexpr int kLdsStage = kRing * kRowWords;
 constexpr int kLdsTile = kLdsStage + kStage * kRowWords;       // per decoder wave: 2 groups per page
-constexpr int kLdsFlags = kLdsTile + kProducerWaves * kRowWords;
-constexpr int kFlagRing = 0;                         // [kRing] code row index + 1
+constexpr int kLdsFlags = kLdsTile + kDecoderWaves * kRowWords;
+constexpr int kFlagRing = 0;                         // [kRing] payload row index + 1
 constexpr int kFlagReady = kFlagRing + kRing;        // [kStage] unit + 1: scales decrypted
 constexpr int kFlagFree = kFlagReady + kStage;       // [kStage] unit + 1: scales consumed
 constexpr int kFlagCount = kFlagFree + kStage;       // [kStage] code rows that took their scales
-constexpr int kFlagMacUsed = kFlagCount + kStage;    // code rows absorbed by the verify wave
+constexpr int kFlagMacUsed = kFlagCount + kStage;    // payload rows absorbed by the verify wave
 constexpr int kFlagTask = kFlagMacUsed + 1;          // next row to hand out
 constexpr int kFlagStatus = kFlagTask + 1;           // [64] verdicts
-constexpr int kNumFlags = kFlagStatus + 64;
-constexpr int kLdsPtrs = kLdsFlags + kNumFlags + (kNumFlags & 1);  // [2][64] output pointers
+constexpr int kNumFlags = (kFlagStatus + 64 + 1) & ~1;  // even: the pointer table after it is 8-byte aligned
+constexpr int kLdsPtrs = kLdsFlags + kNumFlags;      // [2][64] output pointers (K, V)
 constexpr int kLdsLayouts = kLdsPtrs + 2 * 2 * 64;   // [9] Layout, one per header flags value
 constexpr int kLayoutWords = (int)(sizeof(Layout) / 4);
 constexpr int kLdsWords = kLdsLayouts + 9 * kLayoutWords;
 static_assert(sizeof(Layout) % 4 == 0, "Layout is copied word by word");
+static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
+static_assert(kLdsPtrs % 2 == 0, "pointer table must be 8-byte aligned");
+static_assert(kStage > kLookahead, "a scale row waits for a unit before its own");
 
 __device__ __forceinline__ void load_block(const uint8_t* p, uint32_t w[16]) {
 #pragma unroll
@@ -183,7 +192,8 @@ struct Task {
     int32_t scale;    // 1: scale row of unit u
     int32_t u, j;     // unit in section, code block in unit
     int32_t g;        // unit index among the page's quantized units (staging order)
-    int32_t cidx;     // code row index (payload order)
+    int32_t cidx;     // code row index (payload order of the code rows)
+    int32_t mrow;     // payload row of a code row (its place in the ring)
     int32_t block;    // payload block index (keystream counter - 1)
     SecRows s;
 };
@@ -230,6 +240,7 @@ __device__ __forceinline__ Task task_info(const Layout& lay, int32_t t) {
             }
             k.g = s.qunit_begin + k.u;
             k.cidx = cb + k.u * s.nblk + k.j;
+            k.mrow = k.cidx + qb;  // a section's codes follow the scale rows of the sections before it
             k.block = k.scale ? (int32_t)(s.s_off / 64u) + k.u : (int32_t)(s.q_off / 64u) + k.u * s.nblk + k.j;
             k.s = s;
         }
@@ -251,12 +262,6 @@ __device__ __forceinline__ int32_t total_tasks(const Layout& lay) {
     return t;
 }
 
-// Byte offset of group G of a section inside the page's K or V buffer.
-__device__ __forceinline__ uint32_t group_offset(const SecRows& s, int32_t G, int32_t head_dim) {
-    const int32_t vec = G / s.gpv, gi = G - vec * s.gpv;
-    return (uint32_t)vec * (uint32_t)head_dim * 2u + (uint32_t)(s.col + gi * 16) * 2u;
-}
-
 struct DecoderCtx {
     const IngressParams* p;
     const uint8_t* pay;     // this lane's page payload
@@ -264,23 +269,20 @@ struct DecoderCtx {
     ChaChaNonceCache nc;
     uint32_t* lds;
     uint32_t* tile;         // this wave's dequantized tile
+    PageQuads pq;           // this lane's quads in a row slot
     int lane;
-};
+    // Transposed tile stores: store k (0..3) writes quad (lane & 3) of page
+    // 16 k + (lane >> 2), whose output pointer is entry 16 k + (lane >> 2)
+    // of the pointer table.  Past the last page of a partial workgroup the
+    // table holds page 0's pointers, and the tile holds page 0's data (those
+    // lanes decode page 0), so every store is unconditional: a store under a
+    // branch makes the compiler wait for all outstanding stores before the
+    // next row's loads.  The quad swizzle of page 16 k + i equals that of
+    // page i, so store k's tile offset is tq0 + 1024 k bytes.
+    uint32_t tq0;
 
-// Stores the wave's tile (two groups G, G + 1 of 64 pages) transposed: lane l
-// writes 16 bytes of page 16 k + (l >> 2).
-__device__ __forceinline__ void store_tile(const DecoderCtx& c, const SecRows& s, int32_t G) {
-    const uint64_t* ptrs = reinterpret_cast<const uint64_t*>(c.lds + kLdsPtrs) + (s.src ? 64 : 0);
-    const int q = c.lane & 3;
-    const uint32_t off = group_offset(s, G + (q >> 1), c.p->head_dim) + 16u * (uint32_t)(q & 1);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int pr = 16 * k + (c.lane >> 2);
-        const uint4 x = lds_quad(c.tile, pr, q);
-        uint8_t* out = reinterpret_cast<uint8_t*>(ptrs[pr]);
-        if (out) stg16(out + off, 0, x);
-    }
-}
+    __device__ __forceinline__ void init_stores() { tq0 = quad_word(lane >> 2, lane & 3) * 4u; }
+};
 
 template <int DT, int KIND>
 __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, uint32_t (&ct)[16],
@@ -289,13 +291,13 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     constexpr int SW = GPB / 2;  // scale words of this row
     const IngressParams& p = *c.p;
     uint32_t* flags = c.lds + kLdsFlags;
-    // ciphertext to the verify wave
-    uint32_t* slot = c.lds + (k.cidx % kRing) * kRowWords;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.cidx - kRing + 1, p.state);
+    // ciphertext to the verify wave, at its place in payload order
+    uint32_t* slot = c.lds + (k.mrow % kRing) * kRowWords;
+    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, p.state);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        lds_put_quad(slot, c.lane, q, make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
-    publish(&flags[kFlagRing + k.cidx % kRing], (uint32_t)k.cidx + 1u);
+        lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
+    publish(&flags[kFlagRing + k.mrow % kRing], (uint32_t)k.mrow + 1u);
     uint32_t pt[16];
     {
         uint32_t ks[16];
@@ -309,10 +311,13 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
         const int slot_s = k.g % kStage;
         wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, p.state);
         const uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
-#pragma unroll
-        for (int t = 0; t < SW; ++t) {
-            const int wd = k.j * SW + t;
-            sc[t] = stage[quad_word(c.lane, wd >> 2) + (wd & 3)];
+        if constexpr (KIND == kSecInt8) {  // words 2j, 2j + 1 of the page's scale row
+            const uint32_t* w = stage + quad_word(c.lane, k.j >> 1) + 2 * (k.j & 1);
+            sc[0] = w[0];
+            sc[1] = w[1];
+        } else {  // words 4j .. 4j + 3
+            const uint4 v = lds_quad(stage, c.lane, k.j);
+            sc[0] = v.x; sc[1] = v.y; sc[2] = v.z; sc[3] = v.w;
         }
         // the last code row of the unit to take its scales frees the slot
         uint32_t old = 0;
@@ -325,7 +330,10 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
             publish(&flags[kFlagFree + slot_s], (uint32_t)k.g + 1u);
         }
     }
-    const int32_t G0 = k.u * 32 + k.j * GPB;
+    // output offsets of the row's groups, walked in (vec, group) order
+    GroupCursor cur = group_cursor(k.u * 32 + k.j * GPB, k.s.gpv, k.s.col, p.head_dim);
+    const uint32_t skip = (uint32_t)(p.head_dim - k.s.gpv * 16) * 2u;
+    const bool to_v = k.s.src != 0;
 #pragma unroll
     for (int pc = 0; pc < GPB / 2; ++pc) {
         uint32_t o[16];
@@ -343,8 +351,23 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            lds_put_quad(c.tile, c.lane, q, make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]));
-        store_tile(c, k.s, G0 + 2 * pc);
+            lds_put_quad_at(c.tile, c.pq.off[q], make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]));
+        const uint32_t off_a = cur.off;
+        cur.step(k.s.gpv, skip);
+        const uint32_t off_b = cur.off;
+        cur.step(k.s.gpv, skip);
+        // lanes 4i, 4i + 1 store the first group's two quads, 4i + 2, 4i + 3 the second's
+        const uint32_t off = ((c.lane & 2) ? off_b : off_a) + 16u * (uint32_t)(c.lane & 1);
+        const uint64_t* ptab = reinterpret_cast<const uint64_t*>(c.lds + kLdsPtrs) + (to_v ? 64 : 0) + (c.lane >> 2);
+        uint4 x[4];
+        uint8_t* out[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            x[s4] = lds_quad_at(c.tile, c.tq0 + 1024u * (uint32_t)s4);
+            out[s4] = reinterpret_cast<uint8_t*>(ptab[16 * s4]);
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) stg16(out[s4] + off, 0, x[s4]);
     }
 }
 
@@ -365,7 +388,7 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
     uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        lds_put_quad(stage, c.lane, q, make_uint4(sc[4 * q], sc[4 * q + 1], sc[4 * q + 2], sc[4 * q + 3]));
+        lds_put_quad_at(stage, c.pq.off[q], make_uint4(sc[4 * q], sc[4 * q + 1], sc[4 * q + 2], sc[4 * q + 3]));
     publish(&flags[kFlagReady + slot_s], (uint32_t)k.g + 1u);
 }
 
@@ -383,6 +406,11 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
     Task k = task_info(lay, t);
     uint32_t ct[16];
     if (k.valid) load_block(c.pay + 64u * (uint32_t)k.block, ct);
+    // The layout, descriptor and pointer-table reads complete here, before
+    // the loop: a load still counted as in flight where the loop begins makes
+    // the compiler wait for every outstanding memory operation wherever the
+    // loop uses its result.
+    __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
@@ -400,100 +428,108 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
     }
 }
 
-// The verify wave's view of the payload: each section's code rows of the
-// workgroup layout from the LDS ring, everything else from the blob.
-struct VerifyFeed {
-    int32_t si, phase, i, cidx, code_begin;
-    uint32_t off;  // payload offset of the next chunk
-
-    __device__ __forceinline__ void fetch(const IngressParams& p, const Layout& lay, bool has_lay,
-                                          const uint8_t* pay, const uint32_t* lds, int lane, uint4 (&x)[4],
-                                          int32_t& tag) {
-        tag = 0;
-        if (has_lay && si < lay.n_sec) {
-            const SecRows s = sec_rows(lay, si, code_begin, 0);
-            if (phase == 0) {
-                const uint32_t* slot = lds + (cidx % kRing) * kRowWords;
-                wait_ge<kDiagIngressWait>(&lds[kLdsFlags + kFlagRing + cidx % kRing], cidx + 1, p.state);
+// Feeder: copies every payload row that is not a code row of the workgroup
+// layout (scale rows, padding; all rows when no page has a usable layout)
+// from the blob into the ring, in payload order, two rows in flight.  It
+// depends only on the verify wave freeing slots, so the rows before any row
+// it waits for are always in the ring already.
+__device__ __forceinline__ void feed_put(const IngressParams& p, uint32_t* lds, const PageQuads& pq, int32_t r,
+                                         const uint4 (&x)[4]) {
+    uint32_t* flags = lds + kLdsFlags;
+    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], r - kRing + 1, p.state);
+    uint32_t* slot = lds + (r % kRing) * kRowWords;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) x[q] = lds_quad(slot, lane, q);
-                tag = cidx + 1;
-                ++cidx;
-                off += 64u;
-                if (++i == s.n_units * s.nblk) {
-                    i = 0;
-                    phase = s.kind != kSecRaw ? 1 : 2;
-                }
-            } else {
-                const uint8_t* q = pay + off;
-                x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
-                off += 64u;
-                if (++i == s.n_units) phase = 2;
-            }
-            if (phase == 2) {
-                code_begin += s.n_units * s.nblk;
-                ++si;
-                phase = 0;
-                i = 0;
-            }
-            return;
-        }
-        const uint8_t* q = pay + off;  // padding (or no usable layout in the workgroup)
-        x[0] = ldg16(q, 0); x[1] = ldg16(q, 1); x[2] = ldg16(q, 2); x[3] = ldg16(q, 3);
-        off += 64u;
-    }
-};
+    for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
+    publish(&flags[kFlagRing + r % kRing], (uint32_t)r + 1u);
+}
 
-// Verdict of one page (cpp:2313-2355).
-__device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t page, const Layout& lay, bool has_lay,
-                               const uint32_t* lds, uint32_t* used, int lane) {
+__device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout& lay, bool has_lay,
+                             const uint8_t* pay, int lane) {
+    PageQuads pq;
+    pq.init(lane);
+    const int32_t total = (int32_t)(p.payload / 64u);
+    // payload rows [cb_i, ce_i) are section i's code rows (decoders)
+    int32_t cb[3], ce[3];
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        const bool on = has_lay && si < lay.n_sec;
+        const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
+        cb[si] = on ? (int32_t)(ZTCP_SEC_FIELD(lay, si, q_off) / 64u) : 0;
+        ce[si] = cb[si] + (on ? ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16)) : 0);
+    }
+    auto next_fed = [&](int32_t r) {
+#pragma unroll
+        for (int si = 0; si < 3; ++si) r = (r >= cb[si] && r < ce[si]) ? ce[si] : r;
+        return r;
+    };
+    // loads past the last row read the last row again (never put)
+    auto load = [&](int32_t r, uint4 (&x)[4]) {
+        const uint8_t* q = pay + 64u * (uint32_t)min(r, total - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = ldg16(q, i);
+    };
+    int32_t ra = next_fed(0);
+    if (ra >= total) return;
+    uint4 a[4], b[4];
+    load(ra, a);
+    int32_t rb = next_fed(ra + 1);
+    load(rb, b);
+#pragma unroll 1
+    for (;;) {
+        feed_put(p, lds, pq, ra, a);
+        if (rb >= total) break;
+        ra = next_fed(rb + 1);
+        load(ra, a);
+        feed_put(p, lds, pq, rb, b);
+        if (ra >= total) break;
+        rb = next_fed(ra + 1);
+        load(rb, b);
+    }
+}
+
+// Verdict of one page (cpp:2313-2355).  The payload's full 64-byte rows
+// come from the ring; its last (payload % 64) bytes and the tag are loaded
+// with the header.
+__device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t page, uint32_t* lds, int lane) {
     const uint8_t* blob = ingress_blob(p, page);
+    const uint8_t* pay = blob + kHeader;
     const uint4 h0 = ldg16(blob, 0), h1 = ldg16(blob, 1);
+    const int32_t total = (int32_t)(p.payload / 64u);
+    const uint32_t tail0 = (uint32_t)total * 64u;
+    const int ntail = (int)((p.payload - tail0) / 16u);  // 0..3 chunks of 16 bytes
+    uint4 tl[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) tl[i] = ldg16(pay + min(tail0 + 16u * (uint32_t)i, p.payload), 0);
+    const uint4 tag = ldg16(pay + p.payload, 0);
+    const uint64_t tok = ingress_token(p, page);
+    const uint32_t layer = ingress_layer(p, page);
     Sip s;
     s.init(p.mk0, p.mk1);
     const uint64_t hdr[4] = {lo64(h0), hi64(h0), lo64(h1), hi64(h1)};
     s.absorb_words<4>(hdr);
-    const uint8_t* pay = blob + kHeader;
-    const int32_t total = (int32_t)(p.payload / 64u);
-    VerifyFeed feed{0, 0, 0, 0, 0, 0u};
-    uint4 x0[4], x1[4], x2[4];
-    int32_t t0 = 0, t1 = 0, t2 = 0;
-    if (total > 0) feed.fetch(p, lay, has_lay, pay, lds, lane, x0, t0);
-    if (total > 1) feed.fetch(p, lay, has_lay, pay, lds, lane, x1, t1);
-#pragma unroll 1
-    for (int32_t c = 0; c < total; c += 3) {
-        if (c + 2 < total) feed.fetch(p, lay, has_lay, pay, lds, lane, x2, t2);
-        s.absorb64(x0);
-        if (t0) publish(used, (uint32_t)t0);
-        if (c + 1 >= total) break;
-        if (c + 3 < total) feed.fetch(p, lay, has_lay, pay, lds, lane, x0, t0);
-        s.absorb64(x1);
-        if (t1) publish(used, (uint32_t)t1);
-        if (c + 2 >= total) break;
-        if (c + 4 < total) feed.fetch(p, lay, has_lay, pay, lds, lane, x1, t1);
-        s.absorb64(x2);
-        if (t2) publish(used, (uint32_t)t2);
-    }
-#pragma unroll 1
-    for (uint32_t o = (uint32_t)total * 64u; o < p.payload; o += 16u) s.absorb(ldg16(pay + o, 0));
+    PageQuads pq;
+    pq.init(lane);
+    DeviceState* st = p.state;
+    __builtin_amdgcn_s_waitcnt(0);
+    mac_rows<kRing, kDiagIngressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
+                                      total);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (i < ntail) s.absorb(tl[i]);
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
-    const uint4 tag = ldg16(pay + p.payload, 0);
     const uint32_t diff = (tag.x ^ (uint32_t)lo) | (tag.y ^ (uint32_t)(lo >> 32)) |
                           (tag.z ^ (uint32_t)hi) | (tag.w ^ (uint32_t)(hi >> 32));
     const uint32_t magic = h0.x & 0xFFFFu, version = (h0.x >> 16) & 0xFFu;
     if (magic != kMagic || version != kVersion) return 1;
-    const uint64_t tok = lo64(h1);
-    if (h0.y != p.exp_tenant || h0.z != p.exp_model || (h0.w & 0xFFFFu) != ingress_layer(p, page) ||
-        tok != ingress_token(p, page))
-        return 2;
+    if (h0.y != p.exp_tenant || h0.z != p.exp_model || (h0.w & 0xFFFFu) != layer || lo64(h1) != tok) return 2;
     if (diff != 0u) return 3;
     if (layout_index(p, h0.x) < 0) return 1;
     return 0;
 }
 
 template <int DT>
-__global__ __launch_bounds__(kFusedThreads) void ingress_fused_kernel(IngressParams p) {
+__global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
@@ -506,7 +542,6 @@ __global__ __launch_bounds__(kFusedThreads) void ingress_fused_kernel(IngressPar
     const int li = layout_index(p, h0.x);
     const uint64_t any_valid = __ballot(active && li >= 0);
     const int li_wg = any_valid ? __builtin_amdgcn_readlane(li, (int)__builtin_ctzll(any_valid)) : -1;
-    const uint64_t rows_mask = __ballot(active && li >= 0 && li == li_wg);
     const bool has_lay = li_wg >= 0;
     // the nine layouts live in LDS: a table in registers or in the kernel
     // arguments would be copied to scratch memory once indexed by a variable
@@ -515,17 +550,23 @@ __global__ __launch_bounds__(kFusedThreads) void ingress_fused_kernel(IngressPar
     uint32_t* flags = lds + kLdsFlags;
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) flags[i] = 0u;
     if (threadIdx.x < 64) {
+        // Pages outside the row pipeline (another layout, invalid flags) get
+        // its stores too: those of another layout are decoded again below,
+        // after every row store has completed; failing pages are zeroed.
         uint64_t* ptrs = reinterpret_cast<uint64_t*>(lds + kLdsPtrs);
-        const bool rows = (rows_mask >> threadIdx.x) & 1ull;
-        ptrs[threadIdx.x] = rows ? reinterpret_cast<uint64_t>(ingress_k(p, page)) : 0ull;
-        ptrs[64 + threadIdx.x] = rows ? reinterpret_cast<uint64_t>(ingress_v(p, page)) : 0ull;
+        uint8_t* k = ingress_k(p, page);
+        uint8_t* v = ingress_v(p, page);
+        ptrs[threadIdx.x] = reinterpret_cast<uint64_t>(k);
+        ptrs[64 + threadIdx.x] = reinterpret_cast<uint64_t>(v ? v : k);
     }
     __syncthreads();
     const Layout& lay = layouts[has_lay ? li_wg : 0];
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
-        flags[kFlagStatus + lane] = (uint32_t)verify_page(p, page, lay, has_lay, lds, &flags[kFlagMacUsed], lane);
-    } else if ((wave & 3) != 0) {  // waves 4 and 8 share the verify wave's SIMD: they idle
+        flags[kFlagStatus + lane] = (uint32_t)verify_page(p, page, lds, lane);
+    } else if (wave == 4) {
+        ingress_feed(p, lds, lay, has_lay, blob + kHeader, lane);
+    } else if ((wave & 3) != 0 && has_lay) {  // waves 8 and 12 share SIMD 0 and idle
         DecoderCtx c;
         c.p = &p;
         c.pay = blob + kHeader;
@@ -536,27 +577,30 @@ __global__ __launch_bounds__(kFusedThreads) void ingress_fused_kernel(IngressPar
         c.lds = lds;
         c.tile = lds + kLdsTile + (wave - 1 - (wave >> 2)) * kRowWords;
         c.lane = lane;
-        if (has_lay) decode_rows<DT>(c, lay);
-        // pages with another valid layout: unit by unit, one page per wave
-        const uint64_t other = __ballot(active && li >= 0 && li != li_wg);
-        if (other) {
-            const int dw = wave - 1 - (wave >> 2);
-            int n = 0;
-#pragma unroll 1
-            for (uint64_t m = other; m; m &= m - 1, ++n) {
-                if (n % kProducerWaves != dw) continue;
-                const int pl = (int)__builtin_ctzll(m);
-                const int lp = __builtin_amdgcn_readlane(li, pl);
-                const Layout& L2 = layouts[lp];
-                const uint32_t a0 = __builtin_amdgcn_readlane(h1.z, pl), a1 = __builtin_amdgcn_readlane(h1.w, pl);
-                const uint32_t a2 = __builtin_amdgcn_readlane(h0.w, pl);
-                const uint32_t m2 = ((a2 & 0xFFFFu) << 16) | (a2 >> 16);
-#pragma unroll 1
-                for (int u = lane; u < L2.n_units; u += 64) decode_unit<DT>(p, L2, page0 + pl, u, a0, a1, m2);
-            }
-        }
+        c.pq.init(lane);
+        c.init_stores();
+        decode_rows<DT>(c, lay);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // every decode store has completed before the verdicts
+    __builtin_amdgcn_s_waitcnt(0);  // every row store has completed
+    __syncthreads();
+    // pages with another valid layout: unit by unit, one page per wave
+    const uint64_t other = __ballot(active && li >= 0 && li != li_wg);
+    if (other) {
+        int n = 0;
+#pragma unroll 1
+        for (uint64_t m = other; m; m &= m - 1, ++n) {
+            if (n % kIngressWaves != wave) continue;
+            const int pl = (int)__builtin_ctzll(m);
+            const int lp = __builtin_amdgcn_readlane(li, pl);
+            const Layout& L2 = layouts[lp];
+            const uint32_t a0 = __builtin_amdgcn_readlane(h1.z, pl), a1 = __builtin_amdgcn_readlane(h1.w, pl);
+            const uint32_t a2 = __builtin_amdgcn_readlane(h0.w, pl);
+            const uint32_t m2 = ((a2 & 0xFFFFu) << 16) | (a2 >> 16);
+#pragma unroll 1
+            for (int u = lane; u < L2.n_units; u += 64) decode_unit<DT>(p, L2, page0 + pl, u, a0, a1, m2);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // every decode store has completed before the zeroing
+    }
     __syncthreads();
     if ((int)threadIdx.x < ppw) {
         const int32_t st = (int32_t)flags[kFlagStatus + threadIdx.x];
@@ -601,9 +645,9 @@ hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     const size_t lds = (size_t)kLdsWords * sizeof(uint32_t);  // above 64 KiB: gfx950 has 160 KiB per CU
     if (dtype == kHotBf16)
-        hipLaunchKernelGGL(ingress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kFusedThreads), lds, s, p);
+        hipLaunchKernelGGL(ingress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
     else
-        hipLaunchKernelGGL(ingress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kFusedThreads), lds, s, p);
+        hipLaunchKernelGGL(ingress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
     return hipGetLastError();
 }
 

@@ -69,6 +69,75 @@ __device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
     __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// ---------------------------------------------------------------------------
+// The MAC wave's side of a ring of row slots holding the payload in order:
+// payload row r sits in slot r % ring_len once flag[slot] = r + 1, and the
+// wave publishes `used` = rows absorbed, which frees their slots.
+// ---------------------------------------------------------------------------
+
+// One fetched row: its 64 bytes for this lane's page and the value of the
+// row's ready flag, read just before the data.  LDS operations of a wave are
+// performed in order, and a row's maker writes it before it releases the
+// row's flag; so when the flag read shows the row, the data read after it
+// holds the row.  Otherwise the row is read again once the flag is set.
+struct MacRow {
+    uint4 x[4];
+    uint32_t f;
+    int32_t slot;  // ring slot (wave-uniform)
+};
+
+__device__ __forceinline__ void mac_fetch(const uint32_t* ring, const uint32_t* ring_flags, const PageQuads& pq,
+                                          int32_t slot, MacRow& r) {
+    r.slot = slot;
+    r.f = __hip_atomic_load(ring_flags + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");  // the data reads stay after the flag read
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + slot * kRowWords, pq.off[q]);
+}
+
+// Absorbs payload row `want - 1` (re-reading it if it was not ready when
+// fetched) and releases its slot.
+template <uint32_t DIAG>
+__device__ __forceinline__ void mac_absorb(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
+                                           uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want) {
+    if ((int32_t)__builtin_amdgcn_readfirstlane(r.f) < want) {
+        wait_ge<DIAG>(ring_flags + r.slot, want, st);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
+    }
+    s.absorb64(r.x);
+    publish(used, (uint32_t)want);
+}
+
+// Absorbs payload rows [0, total) from a ring of RING slots.  Two rows are
+// in flight; a row is fetched right after the absorption that frees its
+// registers, so every read has a whole row's absorption to complete before
+// it is used and no wait lands on a fresh read.  Fetches are unconditional
+// (past the last row they read slots that are never absorbed): a fetch
+// under a branch would leave the buffer in different registers on the two
+// paths, and the copy that joins them would wait for the fresh read.  The
+// caller completes every load it has issued before the call: a load still
+// counted as in flight where the loop begins (a scalar load in particular,
+// as those complete out of order) would turn the loop's LDS waits into full
+// waits.
+template <int RING, uint32_t DIAG>
+__device__ __forceinline__ void mac_rows(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
+                                         uint32_t* used, const PageQuads& pq, Sip& s, int32_t total) {
+    MacRow r0, r1;
+    int32_t slot = 0;
+    auto next_slot = [&]() { const int32_t v = slot; slot = slot == RING - 1 ? 0 : slot + 1; return v; };
+    mac_fetch(ring, ring_flags, pq, next_slot(), r0);
+    mac_fetch(ring, ring_flags, pq, next_slot(), r1);
+#pragma unroll 1
+    for (int32_t c = 0; c < total; c += 2) {
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r0, c + 1);
+        mac_fetch(ring, ring_flags, pq, next_slot(), r0);
+        if (c + 1 >= total) break;
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r1, c + 2);
+        mac_fetch(ring, ring_flags, pq, next_slot(), r1);
+    }
+}
+
 // Row geometry of one section (all values wave-uniform).
 struct SecRows {
     int32_t kind, nblk, rpu, n_units;
