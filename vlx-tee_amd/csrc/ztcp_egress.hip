@@ -4,35 +4,37 @@
 // encode_one_cold_page_into_cpu (cpp:1103-1426) driven by
 // fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004).
 //
-// Work decomposition (one workgroup = up to 64 pages, 12 waves; lane = page
-// in every wave):
+// Work decomposition (one workgroup = up to 64 pages, 16 waves, four per
+// SIMD; lane = page in every wave):
 //   * A "row" is one 64-byte keystream block position of the payload, for all
 //     pages of the workgroup.  Every payload block is exactly one row: a code
 //     row (4 int8 groups, 8 int4 groups or 2 raw groups) or a scale row (the
-//     32 fp16 scales of one unit = 32 groups).  Rows are produced unit by
-//     unit: a unit's code rows, then its scale row.
-//   * Nine producer waves take code rows in order from an LDS counter.  A
-//     code row quantizes its groups (loaded ahead, four at a time, while a
-//     keystream is being computed), stages the scales in LDS, computes the
-//     keystream, XORs, and writes the ciphertext into a ring of row slots in
-//     LDS.  From the slot it stores the row to the blobs transposed: four
+//     32 fp16 scales of one unit = 32 groups).
+//   * Twelve producer waves (on SIMDs 1-3) take code rows in order from an
+//     LDS counter.  A code row quantizes its groups (loaded a row ahead),
+//     stages the scales in LDS, computes the keystream, XORs, and writes the
+//     ciphertext into a ring of row slots in LDS at its place in payload
+//     order.  From the slot it stores the row to the blobs transposed: four
 //     lanes per page, 64 contiguous bytes per page per store.  The wave that
 //     stages a unit's last scales (an LDS counter per staging slot) also
-//     makes the unit's scale row: it encrypts the staged scales and stores
-//     them the same way.
-//   * Wave 0 runs SipHash for one page per lane, at raised priority on a SIMD
-//     of its own (waves 4 and 8, which the dispatcher places on that SIMD,
-//     exit at once).  It absorbs the header, then the payload in order:
-//     code rows straight from the LDS ring (no global read-back), scale rows
-//     from the blobs once their stores have completed.
+//     makes the unit's scale row during its next code row: it encrypts the
+//     staged scales and stores them the same way.
+//   * Wave 0 runs SipHash for one page per lane, at raised priority on SIMD
+//     0.  It absorbs the header, then the payload rows in order from the
+//     ring, so it never reads global memory.  Scale rows reach the ring
+//     through a feeder wave (wave 4, also on SIMD 0): a scale row is stored
+//     long before the MAC wave reaches it (after all of its section's code
+//     rows), and the feeder copies it back from the blob once its stores
+//     have completed.  Waves 8 and 12 exit at once: producers there slow the
+//     MAC chain down more than they add.
 //   * Hand-offs are monotonic LDS counters with workgroup-scope
-//     release/acquire: ring_flag[slot] = code row index + 1 when produced,
-//     mac_used = code rows absorbed (frees ring slots), stage_flag[slot] =
-//     unit + 1 when a scale row has read its staging slot, scale_flag[slot] =
-//     unit + 1 once the scale row's stores have completed.  Every
-//     wait is bounded; an expired wait sets a sticky diagnostic bit and the
-//     kernel still ends.  Waits only point backwards in row order, so
-//     progress never depends on a later row.
+//     release/acquire: ring_flag[slot] = payload row index + 1 when written,
+//     mac_used = rows absorbed (frees ring slots), stage_flag[slot] = unit + 1
+//     when a scale row has read its staging slot, scale_flag[slot] = unit + 1
+//     once the scale row's stores have completed.  Every wait is bounded; an
+//     expired wait sets a sticky diagnostic bit and the kernel still ends.
+//     Waits only point backwards in row order, so progress never depends on
+//     a later row.
 // Requires every section to hold a multiple of 32 groups (Layout::aligned),
 // payload == required and 16-byte aligned pointers; otherwise the host routes
 // the call to the generic kernels.

@@ -68,7 +68,7 @@ constexpr int kLdsWords = kLdsLayouts + 9 * kLayoutWords;
 static_assert(sizeof(Layout) % 4 == 0, "Layout is copied word by word");
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
 static_assert(kLdsPtrs % 2 == 0, "pointer table must be 8-byte aligned");
-static_assert(kStage > kLookahead, "a scale row waits for a unit before its own");
+static_assert(kStage >= kLookahead, "a scale row only waits for units whose code rows come before it");
 
 __device__ __forceinline__ void load_block(const uint8_t* p, uint32_t w[16]) {
 #pragma unroll

@@ -11,13 +11,6 @@
 
 namespace ztcp {
 
-// Waves per workgroup of the fused kernels: the MAC / verify wave, the waves
-// the dispatcher places on its SIMD (4, 8: they exit at once), and the
-// producers on the other three SIMDs.  12 waves leave each wave 168 VGPRs.
-constexpr int kFusedWaves = 12;
-constexpr int kFusedThreads = 64 * kFusedWaves;
-constexpr int kProducerWaves = kFusedWaves - 1 - (kFusedWaves - 1) / 4;
-
 // Sticky device diagnostics (bit flags, or-ed by kernels).
 constexpr uint32_t kDiagEgressWait = 1u;   // a bounded wait of the fused egress kernel expired
 constexpr uint32_t kDiagIngressWait = 2u;  // a bounded wait of the fused ingress kernel expired
