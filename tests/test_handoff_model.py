@@ -38,6 +38,7 @@ def _const(fname, name):
 
 
 NBLK = {"i8": 8, "i4": 4, "raw": 16}
+LATE_SCALE_PUBLISH = False  # planted mistake: publish a stored scale row after the row's staging wait
 CONFIGS = {  # sections (kind, units) of the layouts the kernels meet
     "k8v4": [("i8", 16), ("i8", 16), ("i4", 32)],
     "int4": [("i8", 16), ("i4", 16), ("i4", 32)],
@@ -131,9 +132,12 @@ def egress_model(secs, n_prod, seed):
             tn = st["task"]; st["task"] += 1
             yield "ok"
             c = code[t]
-            if owed is not None:  # scale row made during this row
+            if owed is not None:  # scale row made and published before the row's waits
                 make_scale(owed)
                 yield "ok"
+                if not LATE_SCALE_PUBLISH:
+                    stored.add(owed)
+                    yield "ok"
             if c["quant"]:
                 g = c["g"]
                 yield from wait(lambda: stage_flag[g % KSTAGE] >= g - KSTAGE + 1)
@@ -142,7 +146,7 @@ def egress_model(secs, n_prod, seed):
                 assert stage_units[g % KSTAGE] == g, "staging slot still holds another unit"
                 staged[g] = staged.get(g, 0) + 1
                 yield "ok"
-            if owed is not None:
+            if owed is not None and LATE_SCALE_PUBLISH:
                 stored.add(owed)
                 yield "ok"
             m = c["m"]
@@ -291,18 +295,30 @@ def ingress_model(secs, n_dec, seed, padding=0):
 
 
 @pytest.mark.parametrize("cfg", sorted(CONFIGS))
-@pytest.mark.parametrize("waves", [1, 3, 12])
+@pytest.mark.parametrize("waves", [1, 3, 12, 48])
 def test_egress_handoffs(cfg, waves):
     for seed in range(3):
         assert egress_model(CONFIGS[cfg], waves, seed), f"deadlock {cfg} waves={waves} seed={seed}"
 
 
 @pytest.mark.parametrize("cfg", sorted(CONFIGS))
-@pytest.mark.parametrize("waves", [1, 3, 12])
+@pytest.mark.parametrize("waves", [1, 3, 12, 48])
 def test_ingress_handoffs(cfg, waves):
     for seed in range(3):
         assert ingress_model(CONFIGS[cfg], waves, seed), f"deadlock {cfg} waves={waves} seed={seed}"
         assert ingress_model(CONFIGS[cfg], waves, seed + 100, padding=5)
+
+
+def test_egress_model_catches_a_late_scale_publication():
+    """A planted mistake: a wave that publishes its scale row only after its
+    next row's staging wait can hold up the feeder while it waits; with
+    enough waves in flight the model finds the deadlock."""
+    global LATE_SCALE_PUBLISH
+    LATE_SCALE_PUBLISH = True
+    try:
+        assert not all(egress_model(CONFIGS["k8v4"], 48, seed) for seed in range(5))
+    finally:
+        LATE_SCALE_PUBLISH = False
 
 
 def test_model_catches_a_staging_ring_smaller_than_the_lookahead():

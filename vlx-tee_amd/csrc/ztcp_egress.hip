@@ -266,6 +266,10 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     if (make_scale) scale_row(c, unit_done);
     st.double_rounds<4>();
     if (kind == kSecInt4) quant_half<DT, 4>(w, pt + 8, sc + 2);
+    // the scale row's stores were issued four double rounds ago; publishing
+    // them before any wait of this row keeps the feeder (and through it the
+    // MAC wave) from depending on this row's waits
+    if (make_scale) publish_scale(flags, unit_done.g);
     if (nxt.valid) load_half(p, c.pg, nxt, 0, w);
     st.double_rounds<5>();
     if (kind != kSecRaw) {
@@ -283,7 +287,6 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     }
     uint32_t ks[16];
     st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
-    if (make_scale) publish_scale(flags, unit_done.g);
     uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
     wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, p.state);
 #pragma unroll

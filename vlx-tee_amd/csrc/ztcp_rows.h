@@ -95,31 +95,41 @@ __device__ __forceinline__ void mac_fetch(const uint32_t* ring, const uint32_t* 
     for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + slot * kRowWords, pq.off[q]);
 }
 
-// Absorbs payload row `want - 1` (re-reading it if it was not ready when
-// fetched) and releases its slot.
+// Absorbs payload row `want - 1` and releases its slot.  `ready` says
+// whether the row's flag read already showed the row; otherwise the row is
+// read again once the flag is set.
 template <uint32_t DIAG>
 __device__ __forceinline__ void mac_absorb(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
-                                           uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want) {
-    if ((int32_t)__builtin_amdgcn_readfirstlane(r.f) < want) {
+                                           uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want,
+                                           bool ready) {
+    if (!ready) {
         wait_ge<DIAG>(ring_flags + r.slot, want, st);
 #pragma unroll
         for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
     }
     s.absorb64(r.x);
     publish(used, (uint32_t)want);
 }
 
+__device__ __forceinline__ bool mac_ready(const MacRow& r, int32_t want) {
+    return (int32_t)__builtin_amdgcn_readfirstlane(r.f) >= want;
+}
+
 // Absorbs payload rows [0, total) from a ring of RING slots.  Two rows are
 // in flight; a row is fetched right after the absorption that frees its
 // registers, so every read has a whole row's absorption to complete before
-// it is used and no wait lands on a fresh read.  Fetches are unconditional
-// (past the last row they read slots that are never absorbed): a fetch
-// under a branch would leave the buffer in different registers on the two
-// paths, and the copy that joins them would wait for the fresh read.  The
-// caller completes every load it has issued before the call: a load still
-// counted as in flight where the loop begins (a scalar load in particular,
-// as those complete out of order) would turn the loop's LDS waits into full
-// waits.
+// it is used and no wait lands on a fresh read.  A row's ready flag is
+// tested right after the previous row's slot is released (a release waits
+// for every LDS operation issued before it, so the flag value is there
+// already), never at the loop head, where the wait would also cover the
+// fetch just issued.  Fetches are unconditional (past the last row they
+// read slots that are never absorbed): a fetch under a branch would leave
+// the buffer in different registers on the two paths, and the copy that
+// joins them would wait for the fresh read.  The caller completes every
+// load it has issued before the call: a load still counted as in flight
+// where the loop begins (a scalar load in particular, as those complete out
+// of order) would turn the loop's LDS waits into full waits.
 template <int RING, uint32_t DIAG>
 __device__ __forceinline__ void mac_rows(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
                                          uint32_t* used, const PageQuads& pq, Sip& s, int32_t total) {
@@ -128,12 +138,15 @@ __device__ __forceinline__ void mac_rows(DeviceState* st, const uint32_t* ring, 
     auto next_slot = [&]() { const int32_t v = slot; slot = slot == RING - 1 ? 0 : slot + 1; return v; };
     mac_fetch(ring, ring_flags, pq, next_slot(), r0);
     mac_fetch(ring, ring_flags, pq, next_slot(), r1);
+    bool ok0 = mac_ready(r0, 1);
 #pragma unroll 1
     for (int32_t c = 0; c < total; c += 2) {
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r0, c + 1);
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r0, c + 1, ok0);
+        const bool ok1 = mac_ready(r1, c + 2);
         mac_fetch(ring, ring_flags, pq, next_slot(), r0);
         if (c + 1 >= total) break;
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r1, c + 2);
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r1, c + 2, ok1);
+        ok0 = mac_ready(r0, c + 3);
         mac_fetch(ring, ring_flags, pq, next_slot(), r1);
     }
 }
