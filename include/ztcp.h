@@ -46,6 +46,19 @@ extern "C" {
 /* QuantPreset (spec:54-59) and RoPEMode (spec:62-67). */
 enum { ZTCP_INT4_SYM = 1, ZTCP_K8V4_ASYM = 2, ZTCP_FP8_ONLY = 3 };
 enum { ZTCP_QUANTIZE_ALL = 0, ZTCP_PRESERVE_FP8 = 1, ZTCP_PRESERVE_RAW = 2 };
+/* Extension presets and RoPE mode (no counterpart in the reference, which
+ * rejects these header flags; same header, framing, cipher and MAC):
+ *   ZTCP_K8V4_ASYM_G64   K: int8 asymmetric per 64 elements (fp16 scale + u16
+ *                        zero point), V: int4 symmetric per 32 elements
+ *   ZTCP_FP8_E4M3        K and V: OCP FP8 e4m3 per 16 elements (fp16 scale
+ *                        = amax / 448, saturating round-to-nearest-even)
+ *   ZTCP_INT4_SYM_G32    K and V: int4 symmetric per 32 elements
+ *   ZTCP_PRESERVE_E4M3   the RoPE columns as e4m3 per 16 elements
+ * A group must not straddle a section: the extension kinds need section
+ * widths divisible by 64 (int8 asymmetric) or 32 (int4 per 32); otherwise the
+ * sizing functions return (size_t)-1 and egress returns ZTCP_EINVAL. */
+enum { ZTCP_K8V4_ASYM_G64 = 4, ZTCP_FP8_E4M3 = 5, ZTCP_INT4_SYM_G32 = 6 };
+enum { ZTCP_PRESERVE_E4M3 = 3 };
 enum { ZTCP_HOT_FP16 = 0, ZTCP_HOT_BF16 = 1 };
 
 /* Integrity verdicts: the reference's per-page status codes (cpp:2056-2057). */
@@ -63,6 +76,9 @@ enum { ZTCP_HOT_FP16 = 0, ZTCP_HOT_BF16 = 1 };
 #define ZTCP_ASYNC 0x1u          /* enqueue only; verdicts land in page_status */
 #define ZTCP_PER_PAGE 0x2u       /* extension: keep verified pages, zero failing ones;
                                     default is the reference's all-or-nothing */
+#define ZTCP_EXT_LAYOUTS 0x4u    /* extension: accept the extension presets / RoPE
+                                    mode in headers; without it they fail with
+                                    status 1, as the reference's flags check does */
 
 typedef struct ztcp_geometry {
     int64_t num_tokens;   /* tokens per page */
@@ -109,7 +125,8 @@ typedef struct ztcp_page_desc {
 } ztcp_page_desc;
 
 /* Payload bytes padded to 4 (spec:203-246, what nfc passes as
- * expected_payload_bytes); (size_t)-1 for invalid preset / rope_mode. */
+ * expected_payload_bytes); (size_t)-1 for invalid preset / rope_mode.  The
+ * extension presets 4..6 and RoPE mode 3 are sized as well. */
 size_t ztcp_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
 /* Unpadded minimum payload for header flags: required_payload_bytes_for_flags
  * (cpp:1439-1474); (size_t)-1 for invalid flags. */
@@ -172,8 +189,11 @@ int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
  * every amax the FP16 and BF16 hot dtypes can produce, the fast scale (a
  * corrected quotient) equals fp16(amax / 127) and fp16(amax / 7) by IEEE
  * division whenever it is a normal fp16 value, and the Newton-refined
- * reciprocal equals 1 / s for every positive finite fp16 scale.  Returns the
- * number of violations (0 = pass) or a negative error.  A test hook like the
+ * reciprocal equals 1 / s for every positive finite fp16 scale; and the
+ * hardware e4m3 conversions (v_cvt_pk_fp8_f32, v_cvt_f32_fp8) the extension
+ * kinds use equal the bit-exact software conversions on every bf16 pattern,
+ * its neighbours and all 256 codes.  Returns the number of violations
+ * (0 = pass) or a negative error.  A test hook like the
  * reference's (cpp:2499-2538); it has no counterpart of its own there. */
 int ztcp_selftest(void);
 

@@ -80,6 +80,12 @@ def lib() -> C.CDLL:
                                          C.c_void_p]
         _lib.zo_dequant_groups.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                                            C.c_size_t, C.c_void_p]
+        _lib.zo_quant_groups_ext.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_size_t, C.c_void_p,
+                                             C.c_void_p]
+        _lib.zo_dequant_groups_ext.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_size_t,
+                                               C.c_void_p]
+        _lib.zo_f32_to_e4m3_array.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        _lib.zo_e4m3_to_f32_array.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
     return _lib
 
 
@@ -150,6 +156,47 @@ def dequant_groups(q: np.ndarray, scales: np.ndarray, dtype: int, bits: int) -> 
     n = sc.size
     out = np.empty((n, 16), dtype=np.uint16)
     lib().zo_dequant_groups(_ptr(q), _ptr(sc), dtype, bits, n, _ptr(out))
+    return out
+
+
+# Extension section kinds (no counterpart in the reference):
+# kind -> (elements per group, code bytes per group, parameter bytes per group)
+SEC_E4M3, SEC_INT4G32, SEC_ASYM8 = 3, 4, 5
+EXT_KINDS = {SEC_E4M3: (16, 16, 2), SEC_INT4G32: (32, 16, 2), SEC_ASYM8: (64, 64, 4)}
+
+
+def f32_to_e4m3(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().zo_f32_to_e4m3_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def e4m3_to_f32(c: np.ndarray) -> np.ndarray:
+    c = np.ascontiguousarray(c, dtype=np.uint8)
+    out = np.empty(c.shape, dtype=np.float32)
+    lib().zo_e4m3_to_f32_array(_ptr(c), _ptr(out), c.size)
+    return out
+
+
+def quant_groups_ext(src_bits: np.ndarray, dtype: int, kind: int):
+    """src_bits: [n, ges] uint16 hot patterns -> (codes [n, cb] u8, params [n, 2] u16:
+    fp16 scale bits, zero point)."""
+    ges, cb, _ = EXT_KINDS[kind]
+    s = np.ascontiguousarray(src_bits, dtype=np.uint16).reshape(-1, ges)
+    n = s.shape[0]
+    q = np.empty((n, cb), dtype=np.uint8)
+    prm = np.empty((n, 2), dtype=np.uint16)
+    assert lib().zo_quant_groups_ext(kind, _ptr(s), dtype, n, _ptr(q), _ptr(prm)) == 0
+    return q, prm
+
+
+def dequant_groups_ext(q: np.ndarray, params: np.ndarray, dtype: int, kind: int) -> np.ndarray:
+    ges, cb, _ = EXT_KINDS[kind]
+    q = np.ascontiguousarray(q, dtype=np.uint8).reshape(-1, cb)
+    prm = np.ascontiguousarray(params, dtype=np.uint16).reshape(-1, 2)
+    out = np.empty((q.shape[0], ges), dtype=np.uint16)
+    assert lib().zo_dequant_groups_ext(kind, _ptr(q), _ptr(prm), dtype, q.shape[0], _ptr(out)) == 0
     return out
 
 

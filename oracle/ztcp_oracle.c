@@ -281,28 +281,204 @@ void zo_dequant_group16_int4(const uint8_t q[8], uint16_t scale_f16, int dtype,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Extension codes (no counterpart in the reference; defined by this codec). */
+/* They follow profile S's shape: an fp32 statistic, an fp16 scale rounded  */
+/* once, inv = 1 / f32(scale), codes by round-to-nearest-even, and a        */
+/* dequantization whose product is exact in fp32 followed by one RNE to the  */
+/* hot dtype.                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* fp32 -> OCP FP8 e4m3 ("e4m3fn": bias 7, no infinities, NaN 0x7F/0xFF,
+ * largest finite 448), saturating: |x| >= 448 gives +-448, NaN gives 0x7F;
+ * otherwise round to nearest even (subnormal step 2^-9). */
+uint8_t zo_f32_to_e4m3(float x) {
+    if (x != x) return 0x7F;
+    const uint8_t sign = (uint8_t)((f2u(x) >> 24) & 0x80u);
+    const float a = fabsf(x);
+    if (a >= 448.0f) return (uint8_t)(sign | 0x7E);
+    if (a < 0.015625f) { /* below 2^-6: multiples of 2^-9; a * 512 is exact */
+        return (uint8_t)(sign | (uint8_t)nearbyintf(a * 512.0f)); /* 8 -> 0x08 = 2^-6 */
+    }
+    const uint32_t u = f2u(a);
+    int e = (int)(u >> 23) - 127;                /* -6 .. 8 */
+    uint32_t m = (u & 0x7FFFFFu) | 0x800000u;    /* 24-bit significand */
+    uint32_t r = m >> 20, rem = m & 0xFFFFFu;   /* keep 1 + 3 bits */
+    if (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) r++;
+    if (r == 16u) { r = 8u; e++; }
+    return (uint8_t)(sign | (uint8_t)(((uint32_t)(e + 7) << 3) | (r & 7u)));
+}
+
+float zo_e4m3_to_f32(uint8_t c) {
+    const uint32_t e = (c >> 3) & 0xFu, m = c & 7u;
+    float v;
+    if (e == 0xFu && m == 7u) v = u2f(0x7FC00000u);
+    else if (e == 0) v = (float)m * 0.001953125f; /* m * 2^-9, exact */
+    else v = u2f(((e + 120u) << 23) | (m << 20));
+    return (c & 0x80u) ? -v : v;
+}
+
+static float group_amax(const uint16_t* src, int dtype, int n, float* vals) {
+    float amax = 1e-6f;
+    for (int i = 0; i < n; ++i) {
+        float v = hot_to_f32(src[i], dtype);
+        vals[i] = v;
+        float av = fabsf(v);
+        if (av > amax) amax = av;
+    }
+    return amax;
+}
+
+/* FP8 e4m3, 16-element group: s = fp16(amax / 448), codes e4m3(v * inv).
+ * A NaN product (0 * inf when the scale underflows to 0, or a NaN input)
+ * gives code 0, as the reference's integer conversion of NaN gives code 0
+ * in its int8 quantizer (cpp:735-753): a group too small for an fp16 scale
+ * decodes to zeros, never to NaN. */
+void zo_quant_group16_e4m3(const uint16_t* src, int dtype, uint8_t q[16],
+                           uint16_t* scale_f16) {
+    float vals[16];
+    const float amax = group_amax(src, dtype, 16, vals);
+    const uint16_t sh = zo_f32_to_f16(amax / 448.0f);
+    *scale_f16 = sh;
+    const float inv = 1.0f / zo_f16_to_f32(sh);
+    for (int i = 0; i < 16; ++i) {
+        const float x = vals[i] * inv;
+        q[i] = x != x ? 0 : zo_f32_to_e4m3(x);
+    }
+}
+
+void zo_dequant_group16_e4m3(const uint8_t q[16], uint16_t scale_f16, int dtype,
+                             uint16_t* dst) {
+    const float s = zo_f16_to_f32(scale_f16);
+    for (int i = 0; i < 16; ++i) dst[i] = f32_to_hot(zo_e4m3_to_f32(q[i]) * s, dtype);
+}
+
+/* INT4 symmetric over a 32-element group: the int4 formula of cpp:806-824
+ * with the absmax taken over 32 elements; 16 code bytes, one fp16 scale. */
+void zo_quant_group32_int4(const uint16_t* src, int dtype, uint8_t q[16],
+                           uint16_t* scale_f16) {
+    float vals[32];
+    const float amax = group_amax(src, dtype, 32, vals);
+    const uint16_t sh = zo_f32_to_f16(amax / 7.0f);
+    *scale_f16 = sh;
+    const float inv = 1.0f / zo_f16_to_f32(sh);
+    for (int i = 0; i < 16; ++i) {
+        int u0 = f32_to_int_x86(nearbyintf(vals[2 * i] * inv) + 8.0f);
+        int u1 = f32_to_int_x86(nearbyintf(vals[2 * i + 1] * inv) + 8.0f);
+        u0 = u0 < 0 ? 0 : (u0 > 15 ? 15 : u0);
+        u1 = u1 < 0 ? 0 : (u1 > 15 ? 15 : u1);
+        q[i] = (uint8_t)((u0 & 0x0F) | ((u1 & 0x0F) << 4));
+    }
+}
+
+void zo_dequant_group32_int4(const uint8_t q[16], uint16_t scale_f16, int dtype,
+                             uint16_t* dst) {
+    zo_dequant_group16_int4(q, scale_f16, dtype, dst);
+    zo_dequant_group16_int4(q + 8, scale_f16, dtype, dst + 16);
+}
+
+/* INT8 asymmetric over a 64-element group.  The range always includes 0:
+ * lo = min(0, min v), hi = max(0, max v); s = fp16(max(1e-6, hi - lo) / 255);
+ * zero point z = clamp(rne(-lo * inv), 0, 255); q = clamp(rne(v * inv) + z,
+ * 0, 255).  Parameters on the wire: fp16 scale, then z as a little-endian
+ * u16.  Dequantized: f32(q - z) * f32(s), exact in fp32, one RNE. */
+void zo_quant_group64_asym8(const uint16_t* src, int dtype, uint8_t q[64],
+                            uint16_t* scale_f16, uint16_t* zero) {
+    float vals[64];
+    float lo = 0.0f, hi = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+        float v = hot_to_f32(src[i], dtype);
+        vals[i] = v;
+        if (v < lo) lo = v;
+        if (v > hi) hi = v;
+    }
+    float range = hi - lo;
+    if (!(range > 1e-6f)) range = 1e-6f;
+    const uint16_t sh = zo_f32_to_f16(range / 255.0f);
+    *scale_f16 = sh;
+    const float inv = 1.0f / zo_f16_to_f32(sh);
+    float zf = nearbyintf(-lo * inv);
+    if (zf < 0.0f) zf = 0.0f;
+    if (zf > 255.0f) zf = 255.0f;
+    const int z = f32_to_int_x86(zf) & 0xFF;
+    *zero = (uint16_t)z;
+    for (int i = 0; i < 64; ++i) {
+        float qf = nearbyintf(vals[i] * inv) + (float)z;
+        if (qf < 0.0f) qf = 0.0f;
+        if (qf > 255.0f) qf = 255.0f;
+        q[i] = (uint8_t)(f32_to_int_x86(qf) & 0xFF);
+    }
+}
+
+void zo_dequant_group64_asym8(const uint8_t q[64], uint16_t scale_f16, uint16_t zero,
+                              int dtype, uint16_t* dst) {
+    const float s = zo_f16_to_f32(scale_f16);
+    for (int i = 0; i < 64; ++i) dst[i] = f32_to_hot((float)((int)q[i] - (int)zero) * s, dtype);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Sizing: cpp:1439-1474 (native, unpadded) and spec:203-246 (padded).      */
 /* ------------------------------------------------------------------------ */
 
+/* Section kinds.  INT8 / INT4 / RAW are the reference's (16-element groups,
+ * cpp:1157-1374); E4M3, INT4G32 and ASYM8 are this codec's extensions. */
+enum { SEC_INT8 = 0, SEC_INT4 = 1, SEC_RAW = 2, SEC_E4M3 = 3, SEC_INT4G32 = 4, SEC_ASYM8 = 5 };
+static const int SEC_GES[6] = {16, 16, 16, 16, 32, 64}; /* elements per group */
+static const int SEC_CB[6] = {16, 8, 32, 16, 16, 64};   /* code bytes per group */
+static const int SEC_PB[6] = {2, 2, 0, 2, 2, 4};        /* scale / zero bytes per group */
+
+/* Presets 1..3 and RoPE modes 0..2 are the reference's (cpp:1447-1449);
+ * presets 4..6 and RoPE mode 3 are extensions:
+ *   4 K8V4_ASYM     K: int8 asymmetric per 64 (ASYM8), V: int4 per 32 (INT4G32)
+ *   5 FP8_E4M3      K and V: e4m3 per 16 (E4M3)
+ *   6 INT4_SYM_G32  K and V: int4 per 32 (INT4G32)
+ *   RoPE mode 3     PRESERVE_E4M3: the RoPE columns as e4m3 per 16.
+ * Returns -1 for flags outside these. */
+static int rope_kind(int64_t rope_mode) {
+    return rope_mode == 1 ? SEC_INT8 : (rope_mode == 2 ? SEC_RAW : (rope_mode == 3 ? SEC_E4M3 : -1));
+}
+static int kmain_kind(int64_t preset) {
+    static const int k[7] = {-1, SEC_INT4, SEC_INT8, SEC_INT8, SEC_ASYM8, SEC_E4M3, SEC_INT4G32};
+    return preset >= 1 && preset <= 6 ? k[preset] : -1;
+}
+static int v_kind(int64_t preset) {
+    static const int k[7] = {-1, SEC_INT4, SEC_INT4, SEC_INT8, SEC_INT4G32, SEC_E4M3, SEC_INT4G32};
+    return preset >= 1 && preset <= 6 ? k[preset] : -1;
+}
+static int flags_valid(int64_t preset, int64_t rope_mode) {
+    return preset >= 1 && preset <= 6 && rope_mode >= 0 && rope_mode <= 3;
+}
+
+/* Bytes of one section of `width` columns over `vecs` vectors; (size_t)-1
+ * when an extension kind's group does not divide the width.  For the
+ * reference's kinds this is the reference's per-column formula
+ * (cpp:1450-1472: one code per column, one scale per whole group). */
+static size_t section_bytes(int kind, int64_t vecs, int64_t width) {
+    switch (kind) {
+    case SEC_RAW: return (size_t)vecs * (size_t)width * 2u;
+    case SEC_INT8: return (size_t)(vecs * width) + (size_t)vecs * (size_t)(width / ZO_GS) * 2u;
+    case SEC_INT4: return (size_t)(vecs * (width / 2)) + (size_t)vecs * (size_t)(width / ZO_GS) * 2u;
+    default:
+        if (width % SEC_GES[kind]) return (size_t)-1;
+        return (size_t)vecs * (size_t)(width / SEC_GES[kind]) * (size_t)(SEC_CB[kind] + SEC_PB[kind]);
+    }
+}
+
 size_t zo_required_payload(int64_t preset, int64_t rope_mode, int64_t vecs,
                            int64_t head_dim, int64_t rope_dim, int has_v) {
-    if (preset < 1 || preset > 3 || rope_mode < 0 || rope_mode > 2) return (size_t)-1;
-    const int64_t nope = head_dim - rope_dim;
-    size_t req = 0;
-    if (rope_mode == 2 && rope_dim > 0) {
-        req += (size_t)vecs * (size_t)rope_dim * 2u;
-    } else if (rope_mode == 1 && rope_dim > 0) {
-        req += (size_t)vecs * (size_t)rope_dim + (size_t)vecs * (size_t)(rope_dim / ZO_GS) * 2u;
+    if (!flags_valid(preset, rope_mode)) return (size_t)-1;
+    size_t req = 0, b;
+    if (rope_mode != 0 && rope_dim > 0) {
+        if ((b = section_bytes(rope_kind(rope_mode), vecs, rope_dim)) == (size_t)-1) return b;
+        req += b;
     }
-    const int64_t kq = rope_mode == 0 ? head_dim : nope;
+    const int64_t kq = rope_mode == 0 ? head_dim : head_dim - rope_dim;
     if (kq > 0) {
-        size_t qb = preset == 1 ? (size_t)(vecs * (kq / 2)) : (size_t)(vecs * kq);
-        req += qb + (size_t)vecs * (size_t)(kq / ZO_GS) * 2u;
+        if ((b = section_bytes(kmain_kind(preset), vecs, kq)) == (size_t)-1) return b;
+        req += b;
     }
     if (has_v) {
-        size_t qb = (preset == 1 || preset == 2) ? (size_t)(vecs * (head_dim / 2))
-                                                 : (size_t)(vecs * head_dim);
-        req += qb + (size_t)vecs * (size_t)(head_dim / ZO_GS) * 2u;
+        if ((b = section_bytes(v_kind(preset), vecs, head_dim)) == (size_t)-1) return b;
+        req += b;
     }
     return req;
 }
@@ -320,10 +496,8 @@ size_t zo_payload_bytes(int64_t preset, int64_t rope_mode, int64_t vecs,
 /* cpp:2418-2461 (decode order), cpp:1146-1374 (section byte maps).          */
 /* ------------------------------------------------------------------------ */
 
-enum { SEC_INT8 = 0, SEC_INT4 = 1, SEC_RAW = 2 };
-
 typedef struct {
-    int kind;        /* SEC_INT8 / SEC_INT4 / SEC_RAW */
+    int kind;        /* SEC_* */
     int src;         /* 0 = K, 1 = V */
     int64_t col;     /* first column */
     int64_t width;   /* columns covered */
@@ -332,17 +506,36 @@ typedef struct {
 static int build_sections(int64_t preset, int64_t rope_mode, int64_t head_dim,
                           int64_t rope_dim, int has_v, zo_section out[3]) {
     int n = 0;
-    if (rope_mode == 2 && rope_dim > 0) {
-        out[n++] = (zo_section){SEC_RAW, 0, 0, rope_dim};
-    } else if (rope_mode == 1 && rope_dim > 0) {
-        out[n++] = (zo_section){SEC_INT8, 0, 0, rope_dim};
-    }
+    if (rope_mode != 0 && rope_dim > 0) out[n++] = (zo_section){rope_kind(rope_mode), 0, 0, rope_dim};
     const int64_t kq = rope_mode == 0 ? head_dim : head_dim - rope_dim;
     const int64_t kc = rope_mode == 0 ? 0 : rope_dim;
-    if (kq > 0) out[n++] = (zo_section){preset == 1 ? SEC_INT4 : SEC_INT8, 0, kc, kq};
-    if (has_v)
-        out[n++] = (zo_section){(preset == 1 || preset == 2) ? SEC_INT4 : SEC_INT8, 1, 0, head_dim};
+    if (kq > 0) out[n++] = (zo_section){kmain_kind(preset), 0, kc, kq};
+    if (has_v) out[n++] = (zo_section){v_kind(preset), 1, 0, head_dim};
     return n;
+}
+
+/* Codes and parameters of group `gi` of a quantized section.  params[0] is
+ * the fp16 scale, params[1] the zero point (ASYM8 only). */
+static void quant_group_kind(int kind, const uint16_t* grp, int dtype, uint8_t* q,
+                             uint16_t params[2]) {
+    switch (kind) {
+    case SEC_INT8: zo_quant_group16_int8(grp, dtype, q, &params[0]); break;
+    case SEC_INT4: zo_quant_group16_int4(grp, dtype, q, &params[0]); break;
+    case SEC_E4M3: zo_quant_group16_e4m3(grp, dtype, q, &params[0]); break;
+    case SEC_INT4G32: zo_quant_group32_int4(grp, dtype, q, &params[0]); break;
+    default: zo_quant_group64_asym8(grp, dtype, q, &params[0], &params[1]); break;
+    }
+}
+
+static void dequant_group_kind(int kind, const uint8_t* q, const uint16_t params[2], int dtype,
+                               uint16_t* out) {
+    switch (kind) {
+    case SEC_INT8: zo_dequant_group16_int8(q, params[0], dtype, out); break;
+    case SEC_INT4: zo_dequant_group16_int4(q, params[0], dtype, out); break;
+    case SEC_E4M3: zo_dequant_group16_e4m3(q, params[0], dtype, out); break;
+    case SEC_INT4G32: zo_dequant_group32_int4(q, params[0], dtype, out); break;
+    default: zo_dequant_group64_asym8(q, params[0], params[1], dtype, out); break;
+    }
 }
 
 /* Plaintext payload of one page (section bytes, then zero padding). */
@@ -363,23 +556,21 @@ static void page_plaintext(const uint16_t* k, const uint16_t* v, int dtype,
             }
             continue;
         }
-        const int64_t groups = w / ZO_GS;
-        const int bpg = secs[s].kind == SEC_INT8 ? 16 : 8;
+        const int kind = secs[s].kind, ges = SEC_GES[kind];
+        const int64_t groups = w / ges;
+        const int bpg = SEC_CB[kind], pb = SEC_PB[kind];
         uint8_t* qb = plain + off;
         uint8_t* sb = qb + (size_t)(vecs * groups * bpg);
         for (int64_t r = 0; r < vecs; ++r) {
             for (int64_t g = 0; g < groups; ++g) {
-                const uint16_t* grp = src + r * head_dim + col + g * ZO_GS;
+                const uint16_t* grp = src + r * head_dim + col + g * ges;
                 const int64_t gi = r * groups + g;
-                uint16_t sc;
-                if (secs[s].kind == SEC_INT8)
-                    zo_quant_group16_int8(grp, dtype, qb + gi * 16, &sc);
-                else
-                    zo_quant_group16_int4(grp, dtype, qb + gi * 8, &sc);
-                memcpy(sb + gi * 2, &sc, 2);
+                uint16_t prm[2] = {0, 0};
+                quant_group_kind(kind, grp, dtype, qb + gi * bpg, prm);
+                memcpy(sb + gi * pb, prm, (size_t)pb); /* little-endian u16s */
             }
         }
-        off += (size_t)(vecs * groups * (bpg + 2));
+        off += (size_t)(vecs * groups * (bpg + pb));
     }
     if (off < payload_len) memset(plain + off, 0, payload_len - off); /* cpp:1411-1422 */
 }
@@ -490,23 +681,21 @@ static int decode_page(const zo_ingress_args* a, int64_t b, uint8_t* plain) {
             }
             continue;
         }
-        const int64_t groups = w / ZO_GS;
-        const int bpg = secs[s].kind == SEC_INT8 ? 16 : 8;
+        const int kind = secs[s].kind, ges = SEC_GES[kind];
+        const int64_t groups = w / ges;
+        const int bpg = SEC_CB[kind], pb = SEC_PB[kind];
         const uint8_t* qb = plain + off;
         const uint8_t* sb = qb + (size_t)(vecs * groups * bpg);
         for (int64_t r = 0; r < vecs; ++r) {
             for (int64_t g = 0; g < groups; ++g) {
                 const int64_t gi = r * groups + g;
-                uint16_t sc;
-                memcpy(&sc, sb + gi * 2, 2);
-                uint16_t* out = dst + r * a->head_dim + col + g * ZO_GS;
-                if (secs[s].kind == SEC_INT8)
-                    zo_dequant_group16_int8(qb + gi * 16, sc, a->dtype, out);
-                else
-                    zo_dequant_group16_int4(qb + gi * 8, sc, a->dtype, out);
+                uint16_t prm[2] = {0, 0};
+                memcpy(prm, sb + gi * pb, (size_t)pb);
+                uint16_t* out = dst + r * a->head_dim + col + g * ges;
+                dequant_group_kind(kind, qb + gi * bpg, prm, a->dtype, out);
             }
         }
-        off += (size_t)(vecs * groups * (bpg + 2));
+        off += (size_t)(vecs * groups * (bpg + pb));
     }
     memset(plain, 0, plen);
     return 0;
@@ -637,4 +826,31 @@ void zo_dequant_groups(const uint8_t* q, const uint16_t* scales, int dtype, int 
         else
             zo_dequant_group16_int4(q + 8 * g, scales[g], dtype, dst + 16 * g);
     }
+}
+
+/* Extension kinds over n groups (kind 3 = E4M3 / 16 elements, 4 = INT4G32 /
+ * 32, 5 = ASYM8 / 64); params holds two u16 per group (scale, zero point). */
+int zo_quant_groups_ext(int kind, const uint16_t* src, int dtype, size_t n, uint8_t* q,
+                        uint16_t* params) {
+    if (kind < SEC_E4M3 || kind > SEC_ASYM8) return -1;
+    for (size_t g = 0; g < n; ++g) {
+        params[2 * g] = params[2 * g + 1] = 0;
+        quant_group_kind(kind, src + (size_t)SEC_GES[kind] * g, dtype, q + (size_t)SEC_CB[kind] * g,
+                         params + 2 * g);
+    }
+    return 0;
+}
+int zo_dequant_groups_ext(int kind, const uint8_t* q, const uint16_t* params, int dtype, size_t n,
+                          uint16_t* dst) {
+    if (kind < SEC_E4M3 || kind > SEC_ASYM8) return -1;
+    for (size_t g = 0; g < n; ++g)
+        dequant_group_kind(kind, q + (size_t)SEC_CB[kind] * g, params + 2 * g, dtype,
+                           dst + (size_t)SEC_GES[kind] * g);
+    return 0;
+}
+void zo_f32_to_e4m3_array(const float* src, uint8_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = zo_f32_to_e4m3(src[i]);
+}
+void zo_e4m3_to_f32_array(const uint8_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = zo_e4m3_to_f32(src[i]);
 }

@@ -50,8 +50,24 @@ void zo_dequant_group16_int8(const uint8_t q[16], uint16_t scale_f16, int dtype,
 void zo_dequant_group16_int4(const uint8_t q[8], uint16_t scale_f16, int dtype,
                              uint16_t* dst);
 
+/* Extension codes (no counterpart in the reference): FP8 e4m3 per 16
+ * elements, int4 per 32, int8 asymmetric per 64 (scale, zero point). */
+uint8_t zo_f32_to_e4m3(float x);
+float zo_e4m3_to_f32(uint8_t c);
+void zo_quant_group16_e4m3(const uint16_t* src, int dtype, uint8_t q[16], uint16_t* scale_f16);
+void zo_dequant_group16_e4m3(const uint8_t q[16], uint16_t scale_f16, int dtype, uint16_t* dst);
+void zo_quant_group32_int4(const uint16_t* src, int dtype, uint8_t q[16], uint16_t* scale_f16);
+void zo_dequant_group32_int4(const uint8_t q[16], uint16_t scale_f16, int dtype, uint16_t* dst);
+void zo_quant_group64_asym8(const uint16_t* src, int dtype, uint8_t q[64], uint16_t* scale_f16,
+                            uint16_t* zero);
+void zo_dequant_group64_asym8(const uint8_t q[64], uint16_t scale_f16, uint16_t zero, int dtype,
+                              uint16_t* dst);
+
 /* ---- sizing ------------------------------------------------------------ */
-/* Unpadded payload bytes for header flags; (size_t)-1 for invalid flags. */
+/* Unpadded payload bytes for header flags; (size_t)-1 for invalid flags.
+ * Presets 1..3 / RoPE modes 0..2 are the reference's; presets 4 (K8V4_ASYM),
+ * 5 (FP8_E4M3), 6 (INT4_SYM_G32) and RoPE mode 3 (PRESERVE_E4M3) are
+ * extensions, valid only where their group size divides the section width. */
 size_t zo_required_payload(int64_t preset, int64_t rope_mode, int64_t vecs,
                            int64_t head_dim, int64_t rope_dim, int has_v);
 /* Payload padded to a 4-byte boundary (the size the Python wrapper passes). */
@@ -106,6 +122,13 @@ void zo_quant_groups(const uint16_t* src, int dtype, int bits, size_t n, uint8_t
                      uint16_t* scales);
 void zo_dequant_groups(const uint8_t* q, const uint16_t* scales, int dtype, int bits,
                        size_t n, uint16_t* dst);
+
+int zo_quant_groups_ext(int kind, const uint16_t* src, int dtype, size_t n, uint8_t* q,
+                        uint16_t* params);
+int zo_dequant_groups_ext(int kind, const uint8_t* q, const uint16_t* params, int dtype, size_t n,
+                          uint16_t* dst);
+void zo_f32_to_e4m3_array(const float* src, uint8_t* dst, size_t n);
+void zo_e4m3_to_f32_array(const uint8_t* src, float* dst, size_t n);
 
 #ifdef __cplusplus
 }

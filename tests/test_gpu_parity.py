@@ -288,7 +288,9 @@ def test_overlap_and_argument_errors(hip):
                                               64, 12288, 0, 0, 0, 0, 0, 1, 2, 3, 4)
     out = torch.zeros((1, 12336), dtype=torch.uint8, device=dev)
     with pytest.raises(RuntimeError, match="preset"):
-        hip.fused_encode_cold_pages_peak_into(k, v, th, out, 4, 1, 64, 12288, 0, 0, 0, 0, 0, 1, 2, 3, 4)
+        hip.fused_encode_cold_pages_peak_into(k, v, th, out, 7, 1, 64, 12288, 0, 0, 0, 0, 0, 1, 2, 3, 4)
+    with pytest.raises(RuntimeError, match="rope_mode"):
+        hip.fused_encode_cold_pages_peak_into(k, v, th, out, 1, 4, 64, 12288, 0, 0, 0, 0, 0, 1, 2, 3, 4)
     with pytest.raises(RuntimeError, match="smaller than required"):
         hip.fused_encode_cold_pages_peak_into(k, v, th, torch.zeros((1, 12332), dtype=torch.uint8,
                                                                     device=dev),

@@ -49,9 +49,38 @@ def test_invalid_flags_sizes(pkg, O):
     import vlx_tee_amd._native as N
 
     g = N.geometry(16, 4, 128, 64, N.HOT_FP16, False)
-    for preset, rm in [(0, 1), (4, 1), (1, 3), (1, -1)]:
+    for preset, rm in [(0, 1), (7, 1), (1, 4), (1, -1)]:
         assert N.lib().ztcp_payload_bytes(C.byref(g), preset, rm) == (1 << 64) - 1
         assert O.required_payload(preset, rm, 64, 128, 64, True) == -1
+    # extension kinds whose group does not divide the section width
+    g = N.geometry(16, 4, 128, 16, N.HOT_FP16, False)   # K main section: 112 columns
+    for preset in (4, 6):
+        assert N.lib().ztcp_payload_bytes(C.byref(g), preset, 1) == (1 << 64) - 1
+        assert O.required_payload(preset, 1, 64, 128, 16, True) == -1
+
+
+def test_extension_sizes_agree(pkg, O):
+    """Native sizing == oracle == Python spec for every extension preset / RoPE mode."""
+    import vlx_tee_amd._native as N
+    from vlx_tee_amd.spec import ColdPageGeometry
+
+    for (T, H, D, R, mla) in [(16, 8, 128, 64, False), (64, 1, 576, 64, True), (4, 2, 64, 32, False),
+                              (2, 2, 128, 0, False), (3, 1, 256, 128, True)]:
+        g = N.geometry(T, H, D, R, N.HOT_BF16, mla)
+        geo = ColdPageGeometry(T, H, D, R, is_mla_single_buffer=mla)
+        for preset in range(1, 7):
+            for rm in range(4):
+                if preset <= 3 and rm <= 2:
+                    continue
+                req = O.required_payload(preset, rm, T * H, D, R, not mla)
+                if req == -1:  # a group wider than its section: rejected by all three
+                    assert N.lib().ztcp_required_payload_bytes(C.byref(g), preset, rm) == (1 << 64) - 1
+                    with pytest.raises(ValueError):
+                        geo.cold_blob_bytes(preset, rm)
+                    continue
+                assert N.lib().ztcp_required_payload_bytes(C.byref(g), preset, rm) == req
+                assert N.lib().ztcp_blob_bytes(C.byref(g), preset, rm) == ((req + 3) & ~3) + 48
+                assert geo.cold_blob_bytes(preset, rm) == ((req + 3) & ~3) + 48
 
 
 def test_required_vs_padded(pkg, O):

@@ -17,7 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libztcp_hip.so"
 # Return codes (include/ztcp.h).
 OK, ERR_HEADER, ERR_AAD, ERR_MAC = 0, 1, 2, 3
 EINVAL, EOVERLAP, EHIP, EDEVICE = -1, -2, -3, -4
-ASYNC, PER_PAGE = 0x1, 0x2
+ASYNC, PER_PAGE, EXT_LAYOUTS = 0x1, 0x2, 0x4
 HOT_FP16, HOT_BF16 = 0, 1
 
 # Every symbol include/ztcp.h declares.

@@ -101,7 +101,7 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
                   int64_t preset, int64_t rope_mode, int64_t expected_payload, const ztcp_aad* aad,
                   uint64_t base_seq, const ztcp_keys* keys, hipStream_t stream) {
     if (!geometry_ok(g) || batch <= 0 || !aad || !keys) return ZTCP_EINVAL;
-    if (preset < 1 || preset > 3 || rope_mode < 0 || rope_mode > 2) return ZTCP_EINVAL;
+    if (!flags_valid(preset, rope_mode)) return ZTCP_EINVAL;
     const int64_t vecs = g->num_tokens * g->num_heads;
     const bool has_v = descs ? !g->is_mla_single_buffer : (v != nullptr);
     Layout lay;
@@ -193,11 +193,14 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
     p.rope_dim = (int32_t)g->rope_dim;
     p.has_v = mla ? 0 : 1;
     bool all_aligned = true;
-    for (int preset = 1; preset <= 3; ++preset) {
-        for (int rm = 0; rm <= 2; ++rm) {
-            const int i = (preset - 1) * 3 + rm;
+    const bool ext = (flags & ZTCP_EXT_LAYOUTS) != 0;
+    for (int preset = 1; preset <= (ext ? 6 : 3); ++preset) {
+        for (int rm = 0; rm <= (ext ? 3 : 2); ++rm) {
+            const int i = (preset - 1) * 4 + rm;
             Layout lay;
-            build_layout(preset, rm, vecs, g->head_dim, g->rope_dim, !mla, lay);
+            // an extension layout whose groups do not divide the geometry is
+            // simply not a valid header for it (status 1)
+            if (!build_layout(preset, rm, vecs, g->head_dim, g->rope_dim, !mla, lay)) continue;
             if (p.payload >= lay.required) p.lay_ok |= 1u << i;
             all_aligned = all_aligned && lay.aligned;
         }

@@ -534,6 +534,25 @@ __device__ __forceinline__ uint32_t quant_group_int4(const uint32_t w[8], uint32
 // only rounding is the final RNE conversion.
 // ---------------------------------------------------------------------------
 
+// NaN outputs as the reference's conversions write them (c10::BFloat16:
+// every NaN is 0x7FC0; c10::Half: sign | 0x7E00); the hardware conversions
+// keep other payloads and, for bf16, the sign.
+template <int DT>
+__device__ __forceinline__ void canonical_nans(uint32_t out[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t lo = out[i] & 0xFFFFu, hi = out[i] >> 16;
+        if constexpr (DT == kHotBf16) {
+            lo = (lo & 0x7FFFu) > 0x7F80u ? 0x7FC0u : lo;
+            hi = (hi & 0x7FFFu) > 0x7F80u ? 0x7FC0u : hi;
+        } else {
+            lo = (lo & 0x7FFFu) > 0x7C00u ? ((lo & 0x8000u) | 0x7E00u) : lo;
+            hi = (hi & 0x7FFFu) > 0x7C00u ? ((hi & 0x8000u) | 0x7E00u) : hi;
+        }
+        out[i] = lo | (hi << 16);
+    }
+}
+
 // 16 int8 codes (4 words) -> 8 packed hot words.
 template <int DT>
 __device__ __forceinline__ void dequant_group_int8(const uint32_t q[4], uint32_t scale_bits,
@@ -566,6 +585,294 @@ __device__ __forceinline__ void dequant_group_int4(const uint32_t q[2], uint32_t
             float b = ((float)((hi >> (8 * i)) & 0xFFu) - 8.0f) * s;
             out[4 * j + i] = pack_hot<DT>(a, b);
         }
+    }
+}
+
+// Whether any of the 32 fp16 halves of a decrypted parameter row is inf or
+// NaN (an asym8 row's zero points, 0..255, never look so).  A finite scale
+// times an integer code is never NaN; a non-finite one makes NaN outputs,
+// which the kernels then rewrite with canonical_nans.
+__device__ __forceinline__ bool params_nonfinite(const uint32_t sc[16]) {
+    uint32_t any = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t e = sc[i] & 0x7C007C00u;
+        any |= ((e & 0xFFFFu) == 0x7C00u) | ((e >> 16) == 0x7C00u);
+    }
+    return any != 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Extension codes (no counterpart in the reference; the oracle's
+// zo_quant_group16_e4m3 / zo_quant_group32_int4 / zo_quant_group64_asym8
+// define them).  Same shape as profile S: an fp32 statistic, an fp16 scale
+// rounded once from an IEEE division, inv = 1 / f32(scale) (IEEE), codes by
+// round-to-nearest-even; dequantization is an exact fp32 product and one RNE.
+// ---------------------------------------------------------------------------
+
+// fp32 -> OCP e4m3 ("e4m3fn") saturating at +-448, round to nearest even.
+// NaN inputs are the caller's (they give +-448 here).
+__device__ __forceinline__ uint32_t f32_to_e4m3_sat(float x) {
+    const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+    const float a = __builtin_fminf(__builtin_fabsf(x), 448.0f);
+    const uint32_t u = __float_as_uint(a);
+    // normal range: keep 3 mantissa bits with RNE; the carry runs into the
+    // exponent, which is rebased from 127 to 7 (120 << 3 = 960)
+    const uint32_t nrm = ((u + 0x7FFFFu + ((u >> 20) & 1u)) >> 20) - 960u;
+    // below 2^-6: multiples of 2^-9 (a * 512 is exact); 8 is the code of 2^-6
+    const uint32_t sub = (uint32_t)__builtin_rintf(a * 512.0f);
+    return sign | (a < 0.015625f ? sub : nrm);
+}
+
+// e4m3 code (bits 0..7 of c) -> fp32, exact; 0x7F / 0xFF -> NaN.  The
+// dequantizers use the hardware form below; this one is what ztcp_selftest
+// compares it with.
+__device__ __forceinline__ float e4m3_to_f32_sw(uint32_t c) {
+    const uint32_t m7 = c & 0x7Fu;
+    const float nrm = __uint_as_float((m7 << 20) + 0x3C000000u);  // exponent rebased 7 -> 127
+    const float sub = (float)(c & 7u) * 0.001953125f;              // m * 2^-9
+    float v = m7 < 8u ? sub : nrm;
+    v = m7 == 0x7Fu ? __builtin_nanf("") : v;
+    return __uint_as_float(__float_as_uint(v) | ((c & 0x80u) << 24));
+}
+
+// Byte B of word c -> fp32 by v_cvt_f32_fp8 (exact: every e4m3 value is an
+// fp32 value).
+template <int B>
+__device__ __forceinline__ float e4m3_byte_to_f32(uint32_t c) {
+    return __builtin_amdgcn_cvt_f32_fp8((int)c, B);
+}
+
+// a * b as a plain fp32 multiply.  For fp16 data the compiler otherwise folds
+// the f16 <-> f32 conversion next to a product into v_fma_mix* with a +0
+// addend, which turns a -0 product into +0; e4m3 has a negative zero code
+// (0x80) that the codec keeps (the integer codes never produce -0).
+template <int DT>
+__device__ __forceinline__ float mul_keep_sign(float a, float b) {
+    if constexpr (DT == kHotFp16) {
+        asm volatile("" : "+v"(a));
+        float r = a * b;
+        asm volatile("" : "+v"(r));
+        return r;
+    }
+    return a * b;
+}
+
+template <int DT>
+__device__ __forceinline__ float group_amax16(const uint32_t w[8]) {
+    float amax = 1e-6f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float a = __builtin_fabsf(hot_lo<DT>(w[i]));
+        const float b = __builtin_fabsf(hot_hi<DT>(w[i]));
+        amax = a > amax ? a : amax;
+        amax = b > amax ? b : amax;
+    }
+    return amax;
+}
+
+// The same conversion by gfx950's v_cvt_pk_fp8_f32 (OCP e4m3, round to
+// nearest even) of a value already clamped to [-448, 448]: two values per
+// instruction, low byte first.  ztcp_selftest checks it against
+// f32_to_e4m3_sat on every bf16 pattern and its neighbours (every rounding
+// tie of e4m3 is a bf16 value).
+__device__ __forceinline__ uint32_t e4m3_pair_hw(float a, float b) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+// Clamp for the conversion; a NaN product (a scale that underflowed to 0, or
+// a NaN element) becomes 0 and so code 0.
+__device__ __forceinline__ float e4m3_operand(float x) {
+    return x != x ? 0.0f : __builtin_amdgcn_fmed3f(x, -448.0f, 448.0f);
+}
+
+// e4m3 codes of one 16-element chunk with inv: 4 words, byte i = element i.
+template <int DT>
+__device__ __forceinline__ void e4m3_codes(const uint32_t w[8], float inv, uint32_t q[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e0 = w[2 * j], e1 = w[2 * j + 1];
+        const uint32_t lo = e4m3_pair_hw(e4m3_operand(mul_keep_sign<DT>(hot_lo<DT>(e0), inv)),
+                                         e4m3_operand(mul_keep_sign<DT>(hot_hi<DT>(e0), inv)));
+        const uint32_t hi = e4m3_pair_hw(e4m3_operand(mul_keep_sign<DT>(hot_lo<DT>(e1), inv)),
+                                         e4m3_operand(mul_keep_sign<DT>(hot_hi<DT>(e1), inv)));
+        q[j] = lo | (hi << 16);
+    }
+}
+
+// FP8 e4m3, 16-element group: s = fp16(amax / 448).  Returns the scale bits.
+template <int DT>
+__device__ __forceinline__ uint32_t quant_group_e4m3(const uint32_t w[8], uint32_t q[4]) {
+    const uint32_t sb = f32_to_f16(group_amax16<DT>(w) / 448.0f);
+    e4m3_codes<DT>(w, 1.0f / f16_to_f32(sb), q);
+    return sb;
+}
+
+// int4 codes of one 16-element chunk with inv (the reference's int4 formula,
+// cpp:806-824): 2 words, element 2i in the low nibble of byte i.
+template <int DT>
+__device__ __forceinline__ void int4_codes(const uint32_t w[8], float inv, uint32_t q[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t e = w[4 * j + i];
+            uint32_t nib[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float v = h ? hot_hi<DT>(e) : hot_lo<DT>(e);
+                float rr = __builtin_rintf(v * inv) + 8.0f;
+                rr = rr != rr ? 0.0f : rr;  // NaN: the x86 conversion gives INT_MIN, clamped to 0
+                rr = rr < 0.0f ? 0.0f : (rr > 15.0f ? 15.0f : rr);
+                nib[h] = (uint32_t)rr;
+            }
+            word |= (nib[0] | (nib[1] << 4)) << (8 * i);
+        }
+        q[j] = word;
+    }
+}
+
+// int4 over a 32-element group (chunks a, b): s = fp16(max(amax_a, amax_b) / 7).
+template <int DT>
+__device__ __forceinline__ uint32_t quant_group32_int4(const uint32_t a[8], const uint32_t b[8], uint32_t q[4]) {
+    const float ma = group_amax16<DT>(a), mb = group_amax16<DT>(b);
+    const uint32_t sb = f32_to_f16((mb > ma ? mb : ma) / 7.0f);
+    const float inv = 1.0f / f16_to_f32(sb);
+    int4_codes<DT>(a, inv, q);
+    int4_codes<DT>(b, inv, q + 2);
+    return sb;
+}
+
+// int8 asymmetric over a 64-element group (4 chunks): lo = min(0, min v),
+// hi = max(0, max v), s = fp16(max(1e-6, hi - lo) / 255), z = clamp(rne(-lo *
+// inv), 0, 255), q = clamp(rne(v * inv) + z, 0, 255); NaN codes are 0.
+// Returns scale bits | zero point << 16 (the group's parameter word).
+//
+// Exact emulation for groups with non-finite elements or a zero / infinite
+// scale (inlined in a cold block, as quant_group_exact).
+template <int DT>
+__device__ __forceinline__ uint32_t asym8_exact(const uint32_t (&w)[4][8], uint32_t q[16]) {
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float v = (i & 1) ? hot_hi<DT>(w[c][i >> 1]) : hot_lo<DT>(w[c][i >> 1]);
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
+        }
+    }
+    float range = hi - lo;
+    range = range > 1e-6f ? range : 1e-6f;
+    const uint32_t sb = f32_to_f16(range / 255.0f);
+    const float inv = 1.0f / f16_to_f32(sb);
+    float zf = __builtin_rintf(-lo * inv);
+    zf = zf != zf ? 0.0f : zf;
+    zf = zf < 0.0f ? 0.0f : (zf > 255.0f ? 255.0f : zf);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t e = w[c][2 * j + (i >> 1)];
+                const float v = (i & 1) ? hot_hi<DT>(e) : hot_lo<DT>(e);
+                float qf = __builtin_rintf(v * inv) + zf;
+                qf = qf != qf ? 0.0f : qf;
+                qf = qf < 0.0f ? 0.0f : (qf > 255.0f ? 255.0f : qf);
+                word |= (uint32_t)qf << (8 * i);
+            }
+            q[4 * c + j] = word;
+        }
+    }
+    return sb | ((uint32_t)zf << 16);
+}
+
+// Fast path (finite elements, a positive finite scale): |v * inv| <= 255 *
+// (1 + 2^-10) (x 1.5 for a subnormal scale), so adding 1.5 * 2^23 rounds
+// v * inv to nearest-even in that same add and the low bits of the sum are
+// rne(v * inv) + 2^22; the zero point is added and the result clamped as
+// integers.  A NaN element turns its sum's exponent bits to all ones; the
+// sums' bits are or-ed together to see it, and such a group takes the exact
+// path (NaN codes are 0 there).  min / max over the elements equal the
+// reference-style compares here: NaN is ignored by both, and a -0 bound
+// gives the same range and zero point as a +0 one.
+template <int DT>
+__device__ __forceinline__ uint32_t quant_group64_asym8(const uint32_t (&w)[4][8], uint32_t q[16]) {
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float a = hot_lo<DT>(w[c][i]), b = hot_hi<DT>(w[c][i]);
+            lo = __builtin_fminf(__builtin_fminf(lo, a), b);
+            hi = __builtin_fmaxf(__builtin_fmaxf(hi, a), b);
+        }
+    }
+    float range = hi - lo;
+    range = range > 1e-6f ? range : 1e-6f;
+    const uint32_t sb = f32_to_f16(range / 255.0f);
+    const bool finite = hi < __builtin_inff() && lo > -__builtin_inff();
+    const float inv = recip_fast(f16_to_f32(sb));
+    float zf = __builtin_rintf(-lo * inv);
+    zf = zf < 0.0f ? 0.0f : (zf > 255.0f ? 255.0f : zf);
+    const uint32_t z = (uint32_t)zf;
+    const uint32_t bias = 0x4B400000u - z;  // bits of 1.5 * 2^23, less the zero point
+    uint32_t seen = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t t[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t e = w[c][2 * j + (i >> 1)];
+                const float v = (i & 1) ? hot_hi<DT>(e) : hot_lo<DT>(e);
+                const uint32_t bits = __float_as_uint(v * inv + 12582912.0f);
+                seen |= bits;
+                const int32_t d = (int32_t)(bits - bias);
+                t[i] = (uint32_t)(d < 0 ? 0 : (d > 255 ? 255 : d));  // v_med3_i32
+            }
+            q[4 * c + j] = pack_low_bytes(t[0], t[1], t[2], t[3]);
+        }
+    }
+    // non-finite elements (a NaN one turns its sum's exponent bits to all
+    // ones), a zero or an infinite scale: the exact path
+    const bool special = !finite || sb == 0u || sb >= 0x7C00u || (seen >> 23) != 0x96u;
+    if (__builtin_expect(special, 0)) return asym8_exact<DT>(w, q);
+    return sb | (z << 16);
+}
+
+// 16 e4m3 codes (4 words) -> 8 packed hot words.
+template <int DT>
+__device__ __forceinline__ void dequant_group_e4m3(const uint32_t q[4], uint32_t scale_bits, uint32_t out[8]) {
+    const float s = f16_to_f32(scale_bits & 0xFFFFu);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        out[2 * j] = pack_hot<DT>(mul_keep_sign<DT>(e4m3_byte_to_f32<0>(q[j]), s),
+                                  mul_keep_sign<DT>(e4m3_byte_to_f32<1>(q[j]), s));
+        out[2 * j + 1] = pack_hot<DT>(mul_keep_sign<DT>(e4m3_byte_to_f32<2>(q[j]), s),
+                                      mul_keep_sign<DT>(e4m3_byte_to_f32<3>(q[j]), s));
+    }
+}
+
+// 16 asym8 codes (4 words) of a group with parameter word (scale | zero << 16)
+// -> 8 packed hot words: hot(f32(q - z) * f32(s)).
+template <int DT>
+__device__ __forceinline__ void dequant_asym8_16(const uint32_t q[4], uint32_t prm, uint32_t out[8]) {
+    const float s = f16_to_f32(prm & 0xFFFFu);
+    const int32_t z = (int32_t)(prm >> 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t w = q[j];
+        const float e0 = (float)((int32_t)(w & 0xFFu) - z) * s;
+        const float e1 = (float)((int32_t)((w >> 8) & 0xFFu) - z) * s;
+        const float e2 = (float)((int32_t)((w >> 16) & 0xFFu) - z) * s;
+        const float e3 = (float)((int32_t)(w >> 24) - z) * s;
+        out[2 * j] = pack_hot<DT>(e0, e1);
+        out[2 * j + 1] = pack_hot<DT>(e2, e3);
     }
 }
 

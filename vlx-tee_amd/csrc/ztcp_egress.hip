@@ -8,8 +8,8 @@
 // SIMD; lane = page in every wave):
 //   * A "row" is one 64-byte keystream block position of the payload, for all
 //     pages of the workgroup.  Every payload block is exactly one row: a code
-//     row (4 int8 groups, 8 int4 groups or 2 raw groups) or a scale row (the
-//     32 fp16 scales of one unit = 32 groups).
+//     row (4 int8 / e4m3 / int4-per-32 groups, 8 int4 groups, 2 raw groups
+//     or 1 asym8 group) or a scale row (the 64 parameter bytes of one unit).
 //   * Twelve producer waves (on SIMDs 1-3) take code rows in order from an
 //     LDS counter.  A code row quantizes its groups (loaded a row ahead),
 //     stages the scales in LDS, computes the keystream, XORs, and writes the
@@ -114,7 +114,7 @@ __device__ __forceinline__ int32_t total_rows(const Layout& lay) {
     for (int si = 0; si < 3; ++si) {
         if (si >= lay.n_sec) continue;
         const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
-        const int32_t rpu = kind == kSecInt8 ? 9 : (kind == kSecInt4 ? 5 : 16);
+        const int32_t rpu = code_rows_per_unit(kind) + (kind != kSecRaw ? 1 : 0);
         t += ZTCP_SEC_FIELD(lay, si, n_units) * rpu;
     }
     return t;
@@ -126,13 +126,13 @@ __device__ __forceinline__ void load_group(const uint8_t* p, uint32_t w[8]) {
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
 }
 
-// Issues the hot loads of half h of a code row: groups [4h, 4h + 4) of the
-// row's 4 (int8), 8 (int4) or 2 (raw) groups.
+// Issues the hot loads of half h of a code row: 16-element chunks
+// [4h, 4h + 4) of the row's 4, 8 (int4, int4 per 32) or 2 (raw) chunks.
 __device__ __forceinline__ void load_half(const EgressParams& p, const EgressPage& pg, const Row& row, int h,
                                           uint32_t (&w)[4][8]) {
-    const int ng = row.s.kind == kSecInt8 ? 4 : (row.s.kind == kSecInt4 ? 8 : 2);
+    const int ng = chunks_per_row(row.s.kind);
     const uint8_t* src = row.s.src ? pg.v : pg.k;
-    GroupCursor cur = group_cursor(row.u * 32 + row.j * ng + 4 * h, row.s.gpv, row.s.col, p.head_dim);
+    GroupCursor cur = group_cursor(row.u * row.s.nblk * ng + row.j * ng + 4 * h, row.s.gpv, row.s.col, p.head_dim);
     const uint32_t skip = (uint32_t)(p.head_dim - row.s.gpv * 16) * 2u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -202,6 +202,26 @@ __device__ __forceinline__ void quant_half(const uint32_t (&w)[4][8], uint32_t* 
     }
 }
 
+// e4m3 groups w[0..3] into pt[0..15] and their scales into sc[0..1].
+template <int DT>
+__device__ __forceinline__ void quant_half_e4m3(const uint32_t (&w)[4][8], uint32_t* pt, uint32_t* sc) {
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+        const uint32_t sa = quant_group_e4m3<DT>(w[i], pt + 4 * i);
+        const uint32_t sbb = quant_group_e4m3<DT>(w[i + 1], pt + 4 * (i + 1));
+        sc[i / 2] = sa | (sbb << 16);
+    }
+}
+
+// Two int4 groups of 32 elements (chunks w[0..1], w[2..3]) into pt[0..7];
+// returns their scales (first in the low half).
+template <int DT>
+__device__ __forceinline__ uint32_t quant_half_int4g32(const uint32_t (&w)[4][8], uint32_t* pt) {
+    const uint32_t sa = quant_group32_int4<DT>(w[0], w[1], pt);
+    const uint32_t sbb = quant_group32_int4<DT>(w[2], w[3], pt + 4);
+    return sa | (sbb << 16);
+}
+
 // Publishes that scale row g is in the blobs, for the MAC wave to read.
 __device__ __forceinline__ void publish_scale(uint32_t* flags, int32_t g) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
@@ -232,16 +252,16 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) 
     publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
 }
 
-// One code row.  w holds the row's first four groups, loaded a row ahead;
-// an int4 row loads its second four into w once the first four are
-// quantized, and uses them after four double rounds.  Every kind of row
+// One code row.  w holds the row's first four chunks, loaded a row ahead;
+// an int4 (or int4 per 32) row loads its second four into w once the first
+// four are quantized, and uses them after four double rounds.  Every kind of row
 // issues the next row's loads at the same point, into the same registers,
 // so that no path has to move a register whose load is still in flight
 // (such a move would make the wave wait for it).  A scale row this wave owes
 // (the last code row of a unit it staged) is made right after this row's
 // groups have arrived and published before this row's only wait that
 // depends on the MAC wave.
-template <int DT>
+template <int DT, int FAM>
 __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt,
                                          uint32_t (&w)[4][8], const Row& unit_done, bool make_scale) {
     const EgressParams& p = *c.p;
@@ -255,17 +275,23 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         quant_half<DT, 8>(w, pt, sc);
     } else if (kind == kSecInt4) {
         quant_half<DT, 4>(w, pt, sc);
-    } else {
+    } else if (FAM == 0 || kind == kSecRaw) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             pt[t] = w[0][t];
             pt[8 + t] = w[1][t];
         }
+    } else if constexpr (FAM == 1) {
+        if (kind == kSecE4m3) quant_half_e4m3<DT>(w, pt, sc);
+        else if (kind == kSecInt4G32) sc[0] = quant_half_int4g32<DT>(w, pt);
+        else sc[0] = quant_group64_asym8<DT>(w, pt);
     }
-    if (kind == kSecInt4) load_half(p, c.pg, row, 1, w);
+    const bool two_halves = kind == kSecInt4 || (FAM == 1 && kind == kSecInt4G32);
+    if (two_halves) load_half(p, c.pg, row, 1, w);
     if (make_scale) scale_row(c, unit_done);
     st.double_rounds<4>();
     if (kind == kSecInt4) quant_half<DT, 4>(w, pt + 8, sc + 2);
+    else if (FAM == 1 && kind == kSecInt4G32) sc[1] = quant_half_int4g32<DT>(w, pt + 8);
     // the scale row's stores were issued four double rounds ago; publishing
     // them before any wait of this row keeps the feeder (and through it the
     // MAC wave) from depending on this row's waits
@@ -276,7 +302,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         // the unit's staging slot is free once unit g - kStage's scale row is done
         uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
         wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
-        const int sw = kind == kSecInt8 ? 2 : 4;  // scale words of this row
+        const int sw = param_words_per_row(kind);  // parameter words of this row: 2, 4 or 1
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             if (t < sw) {
@@ -298,7 +324,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);
 }
 
-template <int DT>
+template <int DT, int FAM>
 __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
     ProducerCtx c;
     c.p = &p;
@@ -336,7 +362,7 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     while (t < total) {
         const int32_t tn = grab();
         const Row nxt = row_info(p.lay, tn);
-        code_row<DT>(c, cur, nxt, w, unit_done, make_scale);
+        code_row<DT, FAM>(c, cur, nxt, w, unit_done, make_scale);
         make_scale = false;
         if (cur.s.kind != kSecRaw) {
             // count the unit's staged code rows; whoever stages the last one
@@ -379,7 +405,7 @@ struct MacPlan {
             const bool on = si < lay.n_sec;
             const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
             const int32_t nu = ZTCP_SEC_FIELD(lay, si, n_units);
-            nc[si] = on ? nu * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16)) : 0;
+            nc[si] = on ? nu * code_rows_per_unit(kind) : 0;
             ns[si] = on && kind != kSecRaw ? nu : 0;
             so[si] = ZTCP_SEC_FIELD(lay, si, s_off);
         }
@@ -487,7 +513,10 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
     }
 }
 
-template <int DT>
+// FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also the
+// extension kinds (e4m3, int4 per 32, asym8).  Separate instantiations keep
+// the extension's registers out of the reference kinds' kernel.
+template <int DT, int FAM>
 __global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
@@ -510,7 +539,7 @@ __global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressPara
         return;
     }
     if ((wave & 3) == 0) return;  // the rest of the MAC wave's SIMD stays idle
-    egress_produce<DT>(p, page0, ppw, lds);
+    egress_produce<DT, FAM>(p, page0, ppw, lds);
 }
 
 }  // namespace
@@ -520,10 +549,16 @@ size_t egress_fused_lds_bytes() { return (size_t)kLdsWords * sizeof(uint32_t); }
 hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) {
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     const size_t lds = egress_fused_lds_bytes();  // above 64 KiB: gfx950 has 160 KiB per CU
-    if (dtype == kHotBf16)
-        hipLaunchKernelGGL(egress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kEgressThreads), lds, s, p);
-    else
-        hipLaunchKernelGGL(egress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kEgressThreads), lds, s, p);
+    bool ext = false;
+    for (int si = 0; si < p.lay.n_sec; ++si) ext = ext || is_extension_kind(p.lay.sec[si].kind);
+    const dim3 g((uint32_t)grid), b(kEgressThreads);
+    if (dtype == kHotBf16) {
+        if (ext) hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 1>), g, b, lds, s, p);
+        else hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 0>), g, b, lds, s, p);
+    } else {
+        if (ext) hipLaunchKernelGGL((egress_fused_kernel<kHotFp16, 1>), g, b, lds, s, p);
+        else hipLaunchKernelGGL((egress_fused_kernel<kHotFp16, 0>), g, b, lds, s, p);
+    }
     return hipGetLastError();
 }
 

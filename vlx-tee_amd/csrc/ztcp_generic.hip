@@ -41,18 +41,32 @@ __device__ __forceinline__ void load_group_u16(const uint8_t* p, uint32_t w[8]) 
     for (int i = 0; i < 8; ++i) w[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
 }
 
+// 16-element chunk g of a section whose vectors hold gpv chunks.
 __device__ __forceinline__ const uint8_t* group_ptr(const uint8_t* base, int64_t head_dim,
                                                     int32_t gpv, int32_t col, int64_t g) {
     const int64_t vec = g / gpv, gg = g % gpv;
     return base + (vec * head_dim + col + gg * 16) * 2;
 }
 
+// One group of any quantized kind: code bytes (up to 64) and the parameter
+// word (fp16 scale, and for asym8 the zero point in bits 16..31).  grp points
+// at the group's first element; its 16, 32 or 64 elements are contiguous.
 template <int DT>
-__device__ void quant_any(const uint32_t w[8], int32_t kind, uint8_t codes[16], uint32_t& sbits) {
-    uint32_t q[4] = {0, 0, 0, 0};
-    if (kind == kSecInt8) sbits = quant_group_int8<DT>(w, q);
-    else sbits = quant_group_int4<DT>(w, q);
-    for (int i = 0; i < 16; ++i) codes[i] = (uint8_t)(q[i / 4] >> (8 * (i % 4)));
+__device__ void quant_any(const uint8_t* grp, int32_t kind, uint8_t codes[64], uint32_t& prm) {
+    uint32_t w[4][8];
+    const int nch = group_elems(kind) / 16;
+    for (int c = 0; c < 4; ++c) {
+        if (c < nch) load_group_u16(grp + 32 * c, w[c]);
+        else for (int i = 0; i < 8; ++i) w[c][i] = 0u;
+    }
+    uint32_t q[16];
+    for (int i = 0; i < 16; ++i) q[i] = 0u;
+    if (kind == kSecInt8) prm = quant_group_int8<DT>(w[0], q);
+    else if (kind == kSecInt4) prm = quant_group_int4<DT>(w[0], q);
+    else if (kind == kSecE4m3) prm = quant_group_e4m3<DT>(w[0], q);
+    else if (kind == kSecInt4G32) prm = quant_group32_int4<DT>(w[0], w[1], q);
+    else prm = quant_group64_asym8<DT>(w, q);
+    for (int i = 0; i < 64; ++i) codes[i] = (uint8_t)(q[i / 4] >> (8 * (i % 4)));
 }
 
 template <int DT>
@@ -79,36 +93,34 @@ __global__ void egress_generic_blocks_kernel(EgressParams p, int64_t nblk) {
                 continue;
             }
             const uint32_t bpg = (uint32_t)code_bytes_per_group(S.kind);
+            const uint32_t ppg = (uint32_t)param_bytes_per_group(S.kind);
+            const int64_t cpg = group_elems(S.kind) / 16;  // 16-element chunks per group
             const uint32_t code_end = S.s_off;
             const uint32_t sc_end = S.q_off + S.bytes;
             // code bytes overlapping [lo, hi)
             uint32_t a = max(lo, S.q_off), b = min(hi, code_end);
             if (a < b) {
                 for (uint32_t g = (a - S.q_off) / bpg; g <= (b - 1 - S.q_off) / bpg; ++g) {
-                    uint32_t w[8];
-                    load_group_u16(group_ptr(src, p.head_dim, S.gpv, S.col, g), w);
-                    uint8_t codes[16];
-                    uint32_t sb;
-                    quant_any<DT>(w, S.kind, codes, sb);
+                    uint8_t codes[64];
+                    uint32_t prm;
+                    quant_any<DT>(group_ptr(src, p.head_dim, S.gpv, S.col, g * cpg), S.kind, codes, prm);
                     for (uint32_t i = 0; i < bpg; ++i) {
                         const uint32_t x = S.q_off + g * bpg + i;
                         if (x >= a && x < b) pt[x - lo] = codes[i];
                     }
                 }
             }
-            // scale bytes overlapping [lo, hi)
+            // parameter bytes overlapping [lo, hi)
             a = max(lo, S.s_off);
             b = min(hi, sc_end);
             if (a < b) {
-                for (uint32_t g = (a - S.s_off) / 2u; g <= (b - 1 - S.s_off) / 2u; ++g) {
-                    uint32_t w[8];
-                    load_group_u16(group_ptr(src, p.head_dim, S.gpv, S.col, g), w);
-                    uint8_t codes[16];
-                    uint32_t sb;
-                    quant_any<DT>(w, S.kind, codes, sb);
-                    for (uint32_t i = 0; i < 2; ++i) {
-                        const uint32_t x = S.s_off + 2u * g + i;
-                        if (x >= a && x < b) pt[x - lo] = (uint8_t)(sb >> (8 * i));
+                for (uint32_t g = (a - S.s_off) / ppg; g <= (b - 1 - S.s_off) / ppg; ++g) {
+                    uint8_t codes[64];
+                    uint32_t prm;
+                    quant_any<DT>(group_ptr(src, p.head_dim, S.gpv, S.col, g * cpg), S.kind, codes, prm);
+                    for (uint32_t i = 0; i < ppg; ++i) {
+                        const uint32_t x = S.s_off + ppg * g + i;
+                        if (x >= a && x < b) pt[x - lo] = (uint8_t)(prm >> (8 * i));
                     }
                 }
             }
@@ -176,8 +188,7 @@ __global__ void ingress_generic_verify_kernel(IngressParams p, int32_t* status) 
     else if ((tlo ^ lo) | (thi ^ hi)) st = 3;
     else {
         const uint32_t preset = flags & 0x0Fu, rope_mode = flags >> 4;
-        if (preset < 1u || preset > 3u || rope_mode > 2u ||
-            !((p.lay_ok >> ((preset - 1u) * 3u + rope_mode)) & 1u))
+        if (!flags_valid(preset, rope_mode) || !((p.lay_ok >> ((preset - 1u) * 4u + rope_mode)) & 1u))
             st = 1;
     }
     status[page] = st;
@@ -196,8 +207,8 @@ __global__ void ingress_generic_decode_kernel(IngressParams p, int64_t groups_pe
         const uint64_t seq = load_u64_bytes(blob + 24);
         const uint32_t flags = (uint32_t)((w0 >> 24) & 0xFFu);
         const uint32_t preset = flags & 0x0Fu, rope_mode = flags >> 4;
-        if (preset < 1u || preset > 3u || rope_mode > 2u) continue;
-        const int li = (int)((preset - 1u) * 3u + rope_mode);
+        if (!flags_valid(preset, rope_mode)) continue;
+        const int li = (int)((preset - 1u) * 4u + rope_mode);
         if (!((p.lay_ok >> li) & 1u)) continue;
         const Layout L = ingress_layout(p, li);
         int si = 0;
@@ -209,7 +220,8 @@ __global__ void ingress_generic_decode_kernel(IngressParams p, int64_t groups_pe
         const uint32_t n2 = (layer << 16) | hg;
         const uint8_t* pay = blob + kHeader;
         uint8_t* out = S.src ? ingress_v(p, page) : ingress_k(p, page);
-        uint8_t* dst = out + ((gi / S.gpv) * p.head_dim + S.col + (gi % S.gpv) * 16) * 2;
+        const int64_t ges = group_elems(S.kind), gpvec = (int64_t)S.gpv * 16 / ges;  // groups per vector
+        uint8_t* dst = out + ((gi / gpvec) * p.head_dim + S.col + (gi % gpvec) * ges) * 2;
         if (S.kind == kSecRaw) {
             uint8_t ks[32];
             keystream_bytes(p.key, n0, n1, n2, S.q_off + (uint32_t)gi * 32u, 32u, ks);
@@ -217,18 +229,29 @@ __global__ void ingress_generic_decode_kernel(IngressParams p, int64_t groups_pe
             continue;
         }
         const uint32_t bpg = (uint32_t)code_bytes_per_group(S.kind);
-        uint8_t ks[16], sk[2];
+        const uint32_t ppg = (uint32_t)param_bytes_per_group(S.kind);
+        uint8_t ks[64], sk[4];
         keystream_bytes(p.key, n0, n1, n2, S.q_off + (uint32_t)gi * bpg, bpg, ks);
-        keystream_bytes(p.key, n0, n1, n2, S.s_off + 2u * (uint32_t)gi, 2u, sk);
-        const uint32_t sbits = (uint32_t)(pay[S.s_off + 2 * gi] ^ sk[0]) |
-                               ((uint32_t)(pay[S.s_off + 2 * gi + 1] ^ sk[1]) << 8);
-        uint32_t q[4] = {0, 0, 0, 0};
+        keystream_bytes(p.key, n0, n1, n2, S.s_off + ppg * (uint32_t)gi, ppg, sk);
+        uint32_t prm = 0;
+        for (uint32_t i = 0; i < ppg; ++i) prm |= (uint32_t)(pay[S.s_off + ppg * gi + i] ^ sk[i]) << (8 * i);
+        uint32_t q[16];
+        for (int i = 0; i < 16; ++i) q[i] = 0u;
         for (uint32_t i = 0; i < bpg; ++i)
             q[i / 4] |= (uint32_t)(pay[S.q_off + gi * bpg + i] ^ ks[i]) << (8 * (i % 4));
-        uint32_t o[8];
-        if (S.kind == kSecInt8) dequant_group_int8<DT>(q, sbits, o);
-        else dequant_group_int4<DT>(q, sbits, o);
-        for (int i = 0; i < 32; ++i) dst[i] = (uint8_t)(o[i / 4] >> (8 * (i % 4)));
+        uint32_t o[32];
+        if (S.kind == kSecInt8) dequant_group_int8<DT>(q, prm, o);
+        else if (S.kind == kSecInt4) dequant_group_int4<DT>(q, prm, o);
+        else if (S.kind == kSecE4m3) dequant_group_e4m3<DT>(q, prm, o);
+        else if (S.kind == kSecInt4G32) {
+            dequant_group_int4<DT>(q, prm, o);
+            dequant_group_int4<DT>(q + 2, prm, o + 8);
+        } else {
+            for (int c = 0; c < 4; ++c) dequant_asym8_16<DT>(q + 4 * c, prm, o + 8 * c);
+        }
+        if ((prm & 0x7C00u) == 0x7C00u)  // an inf / NaN scale: NaN outputs as the reference writes them
+            for (int c = 0; c < 4; ++c) canonical_nans<DT>(o + 8 * c);
+        for (int64_t i = 0; i < 2 * ges; ++i) dst[i] = (uint8_t)(o[i / 4] >> (8 * (i % 4)));
     }
 }
 
@@ -298,8 +321,38 @@ __global__ void selftest_kernel(unsigned int* bad) {
     if (n) atomicAdd(bad, n);
 }
 
+// The hardware e4m3 conversions the kernels use, against the bit-exact
+// software forms (f32_to_e4m3_sat, e4m3_to_f32_sw; the oracle's conversion is
+// the software one, pinned by torch.float8_e4m3fn).  Thread i covers the fp32
+// values (i << 16) | o for five low halves o: every bf16 pattern (which
+// includes every rounding tie of e4m3) and values just above and below them;
+// threads below 256 also decode code i in each byte position.  Violations
+// are counted.
+__global__ void selftest_e4m3_kernel(unsigned int* bad) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 0x10000u) return;
+    uint32_t n = 0;
+    const uint32_t lows[5] = {0x0000u, 0x0001u, 0x7FFFu, 0x8000u, 0xFFFFu};
+    for (int k = 0; k < 5; k += 2) {
+        const float a = __uint_as_float((i << 16) | lows[k]);
+        const float b = __uint_as_float((i << 16) | lows[k < 4 ? k + 1 : k]);
+        const uint32_t hw = e4m3_pair_hw(e4m3_operand(a), e4m3_operand(b));
+        if (a == a && (hw & 0xFFu) != f32_to_e4m3_sat(a)) ++n;
+        if (b == b && (hw >> 8) != f32_to_e4m3_sat(b)) ++n;
+    }
+    if (i < 256u) {  // code i in each byte position of a word
+        const float sw = e4m3_to_f32_sw(i);
+        const float h[4] = {e4m3_byte_to_f32<0>(i), e4m3_byte_to_f32<1>(i << 8), e4m3_byte_to_f32<2>(i << 16),
+                            e4m3_byte_to_f32<3>(i << 24)};
+        for (int b = 0; b < 4; ++b)
+            if (!(h[b] != h[b] && sw != sw) && __float_as_uint(h[b]) != __float_as_uint(sw)) ++n;
+    }
+    if (n) atomicAdd(bad, n);
+}
+
 hipError_t launch_selftest(unsigned int* bad, hipStream_t s) {
     hipLaunchKernelGGL(selftest_kernel, dim3(0x8000 / 256), dim3(256), 0, s, bad);
+    hipLaunchKernelGGL(selftest_e4m3_kernel, dim3(0x10000 / 256), dim3(256), 0, s, bad);
     return hipGetLastError();
 }
 

@@ -60,11 +60,12 @@ constexpr int kFlagCount = kFlagFree + kStage;       // [kStage] code rows that 
 constexpr int kFlagMacUsed = kFlagCount + kStage;    // payload rows absorbed by the verify wave
 constexpr int kFlagTask = kFlagMacUsed + 1;          // next row to hand out
 constexpr int kFlagStatus = kFlagTask + 1;           // [64] verdicts
-constexpr int kNumFlags = (kFlagStatus + 64 + 1) & ~1;  // even: the pointer table after it is 8-byte aligned
+constexpr int kFlagNaN = kFlagStatus + 64;           // [64] 1: the page has an inf / NaN scale
+constexpr int kNumFlags = (kFlagNaN + 64 + 1) & ~1;  // even: the pointer table after it is 8-byte aligned
 constexpr int kLdsPtrs = kLdsFlags + kNumFlags;      // [2][64] output pointers (K, V)
-constexpr int kLdsLayouts = kLdsPtrs + 2 * 2 * 64;   // [9] Layout, one per header flags value
+constexpr int kLdsLayouts = kLdsPtrs + 2 * 2 * 64;   // [kNumLayouts] Layout, one per header flags value
 constexpr int kLayoutWords = (int)(sizeof(Layout) / 4);
-constexpr int kLdsWords = kLdsLayouts + 9 * kLayoutWords;
+constexpr int kLdsWords = kLdsLayouts + kNumLayouts * kLayoutWords;
 static_assert(sizeof(Layout) % 4 == 0, "Layout is copied word by word");
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
 static_assert(kLdsPtrs % 2 == 0, "pointer table must be 8-byte aligned");
@@ -83,13 +84,44 @@ __device__ __forceinline__ void store_group(uint8_t* p, const uint32_t o[8]) {
     stg16(p, 1, make_uint4(o[4], o[5], o[6], o[7]));
 }
 
-// Layout index (preset - 1) * 3 + rope_mode of a header's flags, or -1 when
-// the flags are invalid or the payload is too short for them.
+// Layout index (preset - 1) * 4 + rope_mode of a header's flags, or -1 when
+// the flags are invalid, not enabled for this call (lay_ok: the extension
+// layouts only with ZTCP_EXT_LAYOUTS) or the payload is too short for them.
 __device__ __forceinline__ int layout_index(const IngressParams& p, uint32_t h0x) {
     const uint32_t flags = h0x >> 24, preset = flags & 0x0Fu, rope_mode = flags >> 4;
-    if (preset < 1u || preset > 3u || rope_mode > 2u) return -1;
-    const int li = (int)((preset - 1u) * 3u + rope_mode);
+    if (preset < 1u || preset > 6u || rope_mode > 3u) return -1;
+    const int li = (int)((preset - 1u) * 4u + rope_mode);
     return ((p.lay_ok >> li) & 1u) ? li : -1;
+}
+
+// Extension kinds (family 1 kernels only): compile-time row geometry
+// (ztcp_layout.h) and the dequantization of chunks 2 pc, 2 pc + 1 (32
+// elements, 16 packed hot words) of a decrypted code row pt with the row's
+// parameter words sc.
+template <int KIND>
+struct ExtRows {
+    static constexpr int kChunks = KIND == kSecInt4G32 ? 8 : 4;       // 16-element chunks per row
+    static constexpr int kParamWords = KIND == kSecAsym8 ? 1 : 2;     // parameter words per row
+    static constexpr int kRowsPerUnit = KIND == kSecAsym8 ? 16 : 8;   // code rows per unit
+};
+
+template <int DT, int KIND>
+__device__ __forceinline__ void dequant_pair_ext(const uint32_t* pt, const uint32_t* sc, int pc, uint32_t o[16]) {
+    if constexpr (KIND == kSecInt4G32) {  // group pc: 32 elements, one scale
+        const uint32_t sb = (pc & 1) ? (sc[pc >> 1] >> 16) : (sc[pc >> 1] & 0xFFFFu);
+        dequant_group_int4<DT>(pt + 4 * pc, sb, o);
+        dequant_group_int4<DT>(pt + 4 * pc + 2, sb, o + 8);
+    } else if constexpr (KIND == kSecAsym8) {  // half pc of the row's one group
+        dequant_asym8_16<DT>(pt + 8 * pc, sc[0], o);
+        dequant_asym8_16<DT>(pt + 8 * pc + 4, sc[0], o + 8);
+    } else {  // e4m3: groups 2 pc, 2 pc + 1 of 16 elements
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int gi = 2 * pc + h;
+            const uint32_t sbits = (gi & 1) ? (sc[gi >> 1] >> 16) : (sc[gi >> 1] & 0xFFFFu);
+            dequant_group_e4m3<DT>(pt + 4 * gi, sbits, o + 8 * h);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -97,10 +129,48 @@ __device__ __forceinline__ int layout_index(const IngressParams& p, uint32_t h0x
 // ---------------------------------------------------------------------------
 
 template <int DT, int KIND>
+__device__ __forceinline__ void decode_ext_unit(const IngressParams& p, const uint8_t* pay, uint8_t* out,
+                                                int32_t lu, int32_t gpv, int32_t col, uint32_t q_off,
+                                                uint32_t s_off, uint32_t n0, uint32_t n1, uint32_t n2,
+                                                uint32_t* nan_flag) {
+    using G = ExtRows<KIND>;
+    GroupCursor cur = group_cursor(lu * G::kRowsPerUnit * G::kChunks, gpv, col, p.head_dim);
+    const uint32_t skip = (uint32_t)(p.head_dim - gpv * 16) * 2u;
+    const uint32_t s_unit = s_off + (uint32_t)lu * 64u;
+    uint32_t sc[16];
+    load_block(pay + s_unit, sc);
+    uint32_t ks[16];
+    chacha_block(p.key, 1u + s_unit / 64u, n0, n1, n2, ks);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] ^= ks[i];
+    if (params_nonfinite(sc)) *nan_flag = 1u;
+    const uint32_t code0 = q_off + (uint32_t)lu * (uint32_t)G::kRowsPerUnit * 64u;
+#pragma unroll 1
+    for (int j = 0; j < G::kRowsPerUnit; ++j) {
+        uint32_t ct[16];
+        load_block(pay + code0 + (uint32_t)j * 64u, ct);
+        chacha_block(p.key, 1u + code0 / 64u + (uint32_t)j, n0, n1, n2, ks);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ct[i] ^= ks[i];
+#pragma unroll
+        for (int pc = 0; pc < G::kChunks / 2; ++pc) {
+            uint32_t o[16];
+            dequant_pair_ext<DT, KIND>(ct, sc, pc, o);
+            store_group(out + cur.off, o);
+            cur.step(gpv, skip);
+            store_group(out + cur.off, o + 8);
+            cur.step(gpv, skip);
+        }
+#pragma unroll
+        for (int t = 0; t < 16 - G::kParamWords; ++t) sc[t] = sc[t + G::kParamWords];
+    }
+}
+
+template <int DT, int KIND>
 __device__ __forceinline__ void decode_quant_unit(const IngressParams& p, const uint8_t* pay,
                                                   uint8_t* out, int32_t lu, int32_t gpv,
                                                   int32_t col, uint32_t q_off, uint32_t s_off,
-                                                  uint32_t n0, uint32_t n1, uint32_t n2) {
+                                                  uint32_t n0, uint32_t n1, uint32_t n2, uint32_t* nan_flag) {
     constexpr int GPB = KIND == kSecInt8 ? 4 : 8;
     constexpr int NBLK = 32 / GPB;
     constexpr int CW = KIND == kSecInt8 ? 4 : 2;
@@ -114,6 +184,7 @@ __device__ __forceinline__ void decode_quant_unit(const IngressParams& p, const 
     chacha_block(p.key, 1u + s_unit / 64u, n0, n1, n2, ks);
 #pragma unroll
     for (int i = 0; i < 16; ++i) sc[i] ^= ks[i];
+    if (params_nonfinite(sc)) *nan_flag = 1u;
     const uint32_t code0 = q_off + (uint32_t)(G0 * CW * 4);
 #pragma unroll 1
     for (int j = 0; j < NBLK; ++j) {
@@ -158,9 +229,9 @@ __device__ __forceinline__ void decode_raw_unit(const IngressParams& p, const ui
     }
 }
 
-template <int DT>
+template <int DT, int FAM>
 __device__ __forceinline__ void decode_unit(const IngressParams& p, const Layout& lay, int64_t page, int32_t u,
-                            uint32_t n0, uint32_t n1, uint32_t n2) {
+                            uint32_t n0, uint32_t n1, uint32_t n2, uint32_t* nan_flag) {
     const int si = section_of_unit(lay, u);
     const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
     const int32_t srcsel = ZTCP_SEC_FIELD(lay, si, src);
@@ -172,11 +243,19 @@ __device__ __forceinline__ void decode_unit(const IngressParams& p, const Layout
     const uint8_t* pay = ingress_blob(p, page) + kHeader;
     uint8_t* out = srcsel ? ingress_v(p, page) : ingress_k(p, page);
     if (kind == kSecInt8)
-        decode_quant_unit<DT, kSecInt8>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2);
+        decode_quant_unit<DT, kSecInt8>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2, nan_flag);
     else if (kind == kSecInt4)
-        decode_quant_unit<DT, kSecInt4>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2);
-    else
+        decode_quant_unit<DT, kSecInt4>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2, nan_flag);
+    else if (kind == kSecRaw)
         decode_raw_unit(p, pay, out, lu, gpv, col, q_off, n0, n1, n2);
+    else if constexpr (FAM == 1) {
+        if (kind == kSecE4m3)
+            decode_ext_unit<DT, kSecE4m3>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2, nan_flag);
+        else if (kind == kSecInt4G32)
+            decode_ext_unit<DT, kSecInt4G32>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2, nan_flag);
+        else
+            decode_ext_unit<DT, kSecAsym8>(p, pay, out, lu, gpv, col, q_off, s_off, n0, n1, n2, nan_flag);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -198,13 +277,24 @@ struct Task {
     SecRows s;
 };
 
+template <int FAM>
 __device__ __forceinline__ int32_t div_nblk(int32_t x, int32_t kind) {  // nblk = 8, 4, 16
+    if constexpr (FAM == 1) {
+        const int32_t nblk = code_rows_per_unit(kind);
+        return nblk == 8 ? x / 8 : (nblk == 4 ? x / 4 : x / 16);
+    }
     return kind == kSecInt8 ? x / 8 : (kind == kSecInt4 ? x / 4 : x / 16);
 }
-__device__ __forceinline__ int32_t div_rpu(int32_t x, int32_t kind) {  // nblk + 1 = 9, 5
+template <int FAM>
+__device__ __forceinline__ int32_t div_rpu(int32_t x, int32_t kind) {  // nblk + 1 = 9, 5, 17
+    if constexpr (FAM == 1) {
+        const int32_t nblk = code_rows_per_unit(kind);
+        return nblk == 8 ? x / 9 : (nblk == 4 ? x / 5 : x / 17);
+    }
     return kind == kSecInt8 ? x / 9 : x / 5;
 }
 
+template <int FAM>
 __device__ __forceinline__ Task task_info(const Layout& lay, int32_t t) {
     Task k{};
     int32_t tb = 0, cb = 0, qb = 0;
@@ -218,7 +308,7 @@ __device__ __forceinline__ Task task_info(const Layout& lay, int32_t t) {
             int32_t x = t - tb;
             k.valid = 1;
             if (!quant) {
-                k.u = div_nblk(x, s.kind);
+                k.u = div_nblk<FAM>(x, s.kind);
                 k.j = x - k.u * s.nblk;
             } else {
                 const int32_t pre = min(kLookahead, s.n_units);
@@ -227,13 +317,13 @@ __device__ __forceinline__ Task task_info(const Layout& lay, int32_t t) {
                     k.scale = 1;
                     k.u = x;
                 } else if ((x -= pre) < full * s.rpu) {
-                    const int32_t u = div_rpu(x, s.kind), r = x - u * s.rpu;
+                    const int32_t u = div_rpu<FAM>(x, s.kind), r = x - u * s.rpu;
                     k.scale = r == s.nblk;
                     k.u = k.scale ? u + kLookahead : u;
                     k.j = k.scale ? 0 : r;
                 } else {
                     x -= full * s.rpu;
-                    const int32_t u = div_nblk(x, s.kind);
+                    const int32_t u = div_nblk<FAM>(x, s.kind);
                     k.u = full + u;
                     k.j = x - u * s.nblk;
                 }
@@ -257,7 +347,7 @@ __device__ __forceinline__ int32_t total_tasks(const Layout& lay) {
     for (int si = 0; si < 3; ++si) {
         if (si >= lay.n_sec) continue;
         const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
-        t += ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 9 : (kind == kSecInt4 ? 5 : 16));
+        t += ZTCP_SEC_FIELD(lay, si, n_units) * (code_rows_per_unit(kind) + (kind != kSecRaw ? 1 : 0));
     }
     return t;
 }
@@ -371,6 +461,76 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     }
 }
 
+// code_task for the extension kinds (family 1): the same steps with the
+// kind's row geometry (ExtRows) and dequantizer.
+template <int DT, int KIND>
+__device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k, uint32_t (&ct)[16],
+                                              const Task& nxt) {
+    using G = ExtRows<KIND>;
+    const IngressParams& p = *c.p;
+    uint32_t* flags = c.lds + kLdsFlags;
+    uint32_t* slot = c.lds + (k.mrow % kRing) * kRowWords;
+    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, p.state);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
+    publish(&flags[kFlagRing + k.mrow % kRing], (uint32_t)k.mrow + 1u);
+    uint32_t pt[16];
+    {
+        uint32_t ks[16];
+        chacha_block_cached(p.key, c.nc, 1u + (uint32_t)k.block, c.n0, c.n1, c.n2, ks);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pt[i] = ct[i] ^ ks[i];
+    }
+    if (nxt.valid) load_block(c.pay + 64u * (uint32_t)nxt.block, ct);
+    uint32_t sc[2];
+    const int slot_s = k.g % kStage;
+    wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, p.state);
+    const uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
+    if constexpr (G::kParamWords == 2) {  // words 2j, 2j + 1 of the page's parameter row
+        const uint32_t* w = stage + quad_word(c.lane, k.j >> 1) + 2 * (k.j & 1);
+        sc[0] = w[0];
+        sc[1] = w[1];
+    } else {  // word j
+        sc[0] = stage[quad_word(c.lane, k.j >> 2) + (k.j & 3)];
+        sc[1] = 0u;
+    }
+    uint32_t old = 0;
+    if (c.lane == 0)
+        old = __hip_atomic_fetch_add(&flags[kFlagCount + slot_s], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == (uint32_t)k.s.nblk - 1u) {
+        flags[kFlagCount + slot_s] = 0u;
+        publish(&flags[kFlagFree + slot_s], (uint32_t)k.g + 1u);
+    }
+    GroupCursor cur = group_cursor((k.u * G::kRowsPerUnit + k.j) * G::kChunks, k.s.gpv, k.s.col, p.head_dim);
+    const uint32_t skip = (uint32_t)(p.head_dim - k.s.gpv * 16) * 2u;
+    const bool to_v = k.s.src != 0;
+#pragma unroll
+    for (int pc = 0; pc < G::kChunks / 2; ++pc) {
+        uint32_t o[16];
+        dequant_pair_ext<DT, KIND>(pt, sc, pc, o);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            lds_put_quad_at(c.tile, c.pq.off[q], make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]));
+        const uint32_t off_a = cur.off;
+        cur.step(k.s.gpv, skip);
+        const uint32_t off_b = cur.off;
+        cur.step(k.s.gpv, skip);
+        const uint32_t off = ((c.lane & 2) ? off_b : off_a) + 16u * (uint32_t)(c.lane & 1);
+        const uint64_t* ptab = reinterpret_cast<const uint64_t*>(c.lds + kLdsPtrs) + (to_v ? 64 : 0) + (c.lane >> 2);
+        uint4 x[4];
+        uint8_t* out[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            x[s4] = lds_quad_at(c.tile, c.tq0 + 1024u * (uint32_t)s4);
+            out[s4] = reinterpret_cast<uint8_t*>(ptab[16 * s4]);
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) stg16(out[s4] + off, 0, x[s4]);
+    }
+}
+
 __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, uint32_t (&ct)[16],
                                            const Task& nxt) {
     const IngressParams& p = *c.p;
@@ -383,6 +543,7 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
         for (int i = 0; i < 16; ++i) sc[i] = ct[i] ^ ks[i];
     }
     if (nxt.valid) load_block(c.pay + 64u * (uint32_t)nxt.block, ct);
+    if (params_nonfinite(sc)) flags[kFlagNaN + c.lane] = 1u;
     const int slot_s = k.g % kStage;
     wait_ge<kDiagIngressWait>(&flags[kFlagFree + slot_s], k.g - kStage + 1, p.state);
     uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
@@ -392,7 +553,7 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
     publish(&flags[kFlagReady + slot_s], (uint32_t)k.g + 1u);
 }
 
-template <int DT>
+template <int DT, int FAM>
 __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& lay) {
     uint32_t* flags = c.lds + kLdsFlags;
     auto grab = [&]() -> int32_t {
@@ -403,7 +564,7 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
     };
     const int32_t total = total_tasks(lay);
     int32_t t = grab();
-    Task k = task_info(lay, t);
+    Task k = task_info<FAM>(lay, t);
     uint32_t ct[16];
     if (k.valid) load_block(c.pay + 64u * (uint32_t)k.block, ct);
     // The layout, descriptor and pointer-table reads complete here, before
@@ -414,15 +575,23 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
-        const Task nxt = task_info(lay, tn);
+        const Task nxt = task_info<FAM>(lay, tn);
         if (k.scale)
             scale_task(c, k, ct, nxt);
         else if (k.s.kind == kSecInt8)
             code_task<DT, kSecInt8>(c, k, ct, nxt);
         else if (k.s.kind == kSecInt4)
             code_task<DT, kSecInt4>(c, k, ct, nxt);
-        else
+        else if (FAM == 0 || k.s.kind == kSecRaw)
             code_task<DT, kSecRaw>(c, k, ct, nxt);
+        else if constexpr (FAM == 1) {
+            if (k.s.kind == kSecE4m3)
+                code_task_ext<DT, kSecE4m3>(c, k, ct, nxt);
+            else if (k.s.kind == kSecInt4G32)
+                code_task_ext<DT, kSecInt4G32>(c, k, ct, nxt);
+            else
+                code_task_ext<DT, kSecAsym8>(c, k, ct, nxt);
+        }
         t = tn;
         k = nxt;
     }
@@ -455,7 +624,7 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
         const bool on = has_lay && si < lay.n_sec;
         const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
         cb[si] = on ? (int32_t)(ZTCP_SEC_FIELD(lay, si, q_off) / 64u) : 0;
-        ce[si] = cb[si] + (on ? ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16)) : 0);
+        ce[si] = cb[si] + (on ? ZTCP_SEC_FIELD(lay, si, n_units) * code_rows_per_unit(kind) : 0);
     }
     auto next_fed = [&](int32_t r) {
 #pragma unroll
@@ -528,7 +697,7 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     return 0;
 }
 
-template <int DT>
+template <int DT, int FAM>
 __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
@@ -543,10 +712,10 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     const uint64_t any_valid = __ballot(active && li >= 0);
     const int li_wg = any_valid ? __builtin_amdgcn_readlane(li, (int)__builtin_ctzll(any_valid)) : -1;
     const bool has_lay = li_wg >= 0;
-    // the nine layouts live in LDS: a table in registers or in the kernel
+    // the 24 layouts live in LDS: a table in registers or in the kernel
     // arguments would be copied to scratch memory once indexed by a variable
     Layout* layouts = reinterpret_cast<Layout*>(lds + kLdsLayouts);
-    if (threadIdx.x < 9) layouts[threadIdx.x] = ingress_layout(p, (int)threadIdx.x);
+    if (threadIdx.x < kNumLayouts) layouts[threadIdx.x] = ingress_layout(p, (int)threadIdx.x);
     uint32_t* flags = lds + kLdsFlags;
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) flags[i] = 0u;
     if (threadIdx.x < 64) {
@@ -579,7 +748,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         c.lane = lane;
         c.pq.init(lane);
         c.init_stores();
-        decode_rows<DT>(c, lay);
+        decode_rows<DT, FAM>(c, lay);
     }
     __builtin_amdgcn_s_waitcnt(0);  // every row store has completed
     __syncthreads();
@@ -597,9 +766,31 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
             const uint32_t a2 = __builtin_amdgcn_readlane(h0.w, pl);
             const uint32_t m2 = ((a2 & 0xFFFFu) << 16) | (a2 >> 16);
 #pragma unroll 1
-            for (int u = lane; u < L2.n_units; u += 64) decode_unit<DT>(p, L2, page0 + pl, u, a0, a1, m2);
+            for (int u = lane; u < L2.n_units; u += 64)
+                decode_unit<DT, FAM>(p, L2, page0 + pl, u, a0, a1, m2, &flags[kFlagNaN + pl]);
         }
         __builtin_amdgcn_s_waitcnt(0);  // every decode store has completed before the zeroing
+    }
+    __syncthreads();
+    // Verified pages with an inf / NaN scale (only possible when |values| pass
+    // 65504 times the code range, so with BF16 data): their NaN outputs are
+    // rewritten as the reference's conversions write them.  Every store to
+    // them has completed (the two barriers above).
+#pragma unroll 1
+    for (int pl = 0; pl < ppw; ++pl) {
+        if (flags[kFlagNaN + pl] == 0u || flags[kFlagStatus + pl] != 0u) continue;
+        const int64_t n16 = p.page_bytes / 16;
+        uint8_t* k = ingress_k(p, page0 + pl);
+        uint8_t* v = ingress_v(p, page0 + pl);
+        for (int64_t i = threadIdx.x; i < 2 * n16; i += blockDim.x) {
+            uint8_t* b = i < n16 ? k : v;
+            if (!b) continue;
+            const uint4 x = ldg16(b, i % n16);
+            uint32_t w[8] = {x.x, x.y, x.z, x.w, 0u, 0u, 0u, 0u};
+            canonical_nans<DT>(w);
+            stg16(b, i % n16, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+        __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
     if ((int)threadIdx.x < ppw) {
@@ -644,10 +835,20 @@ __global__ void reset_fail_kernel(DeviceState* st) { st->fail = ~0ull; }
 hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s) {
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     const size_t lds = (size_t)kLdsWords * sizeof(uint32_t);  // above 64 KiB: gfx950 has 160 KiB per CU
-    if (dtype == kHotBf16)
-        hipLaunchKernelGGL(ingress_fused_kernel<kHotBf16>, dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
-    else
-        hipLaunchKernelGGL(ingress_fused_kernel<kHotFp16>, dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
+    // family 1 (the extension kinds) only when the call enables the extension layouts
+    const bool ext = (p.lay_ok >> 12) != 0u;  // bits of presets 4..6 (index (preset - 1) * 4 + rope_mode)
+    const bool ext_rope = (p.lay_ok & 0x888u) != 0u;  // RoPE mode 3 of presets 1..3
+    if (dtype == kHotBf16) {
+        if (ext || ext_rope)
+            hipLaunchKernelGGL((ingress_fused_kernel<kHotBf16, 1>), dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
+        else
+            hipLaunchKernelGGL((ingress_fused_kernel<kHotBf16, 0>), dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
+    } else {
+        if (ext || ext_rope)
+            hipLaunchKernelGGL((ingress_fused_kernel<kHotFp16, 1>), dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
+        else
+            hipLaunchKernelGGL((ingress_fused_kernel<kHotFp16, 0>), dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);
+    }
     return hipGetLastError();
 }
 

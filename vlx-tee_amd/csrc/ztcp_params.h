@@ -58,7 +58,7 @@ struct IngressParams {
     uint32_t blob_bytes;
     uint32_t payload;              // blob_bytes - 48
     int32_t rope_dim, has_v;       // geometry of the page layouts (ingress_layout)
-    uint32_t lay_ok;               // bit (preset - 1) * 3 + rope_mode: payload >= required
+    uint32_t lay_ok;               // bit (preset - 1) * 4 + rope_mode: valid layout, payload >= required
     int32_t n_units;               // generic path: 16-element groups per page
     ChaKey key;
     uint64_t mk0, mk1;
@@ -103,11 +103,11 @@ __device__ __forceinline__ EgressPage egress_page(const EgressParams& p, int64_t
     return e;
 }
 
-// Layout of header flags index li = (preset - 1) * 3 + rope_mode, computed
+// Layout of header flags index li = (preset - 1) * 4 + rope_mode, computed
 // in registers (no table in the kernel arguments).
 __device__ __forceinline__ Layout ingress_layout(const IngressParams& p, int li) {
     Layout L;
-    build_layout(li / 3 + 1, li % 3, p.vecs, p.head_dim, p.rope_dim, p.has_v != 0, L);
+    build_layout(li / 4 + 1, li % 4, p.vecs, p.head_dim, p.rope_dim, p.has_v != 0, L);
     return L;
 }
 

@@ -163,7 +163,7 @@ struct SecRows {
 __device__ __forceinline__ SecRows sec_rows(const Layout& lay, int si, int32_t code_begin, int32_t qunit_begin) {
     SecRows s;
     s.kind = ZTCP_SEC_FIELD(lay, si, kind);
-    s.nblk = s.kind == kSecInt8 ? 8 : (s.kind == kSecInt4 ? 4 : 16);
+    s.nblk = code_rows_per_unit(s.kind);
     s.rpu = s.nblk + (s.kind != kSecRaw ? 1 : 0);
     s.n_units = ZTCP_SEC_FIELD(lay, si, n_units);
     s.code_begin = code_begin;
@@ -182,7 +182,7 @@ __device__ __forceinline__ int32_t total_code_rows(const Layout& lay) {
     for (int si = 0; si < 3; ++si) {
         if (si >= lay.n_sec) continue;
         const int32_t kind = ZTCP_SEC_FIELD(lay, si, kind);
-        t += ZTCP_SEC_FIELD(lay, si, n_units) * (kind == kSecInt8 ? 8 : (kind == kSecInt4 ? 4 : 16));
+        t += ZTCP_SEC_FIELD(lay, si, n_units) * code_rows_per_unit(kind);
     }
     return t;
 }

@@ -93,8 +93,10 @@ def fused_encode_cold_pages_peak_into(
         _check(_hot_dtype(v_pages_opt, "v_pages") == dt and v_pages_opt.device == k_pages.device,
                "v_pages must match k_pages dtype and device")
         _check(v_pages_opt.shape == k_pages.shape, "v_pages shape must match k_pages shape")
-    _check(1 <= preset <= 3, "Invalid preset (must be 1..3)")
-    _check(0 <= rope_mode <= 2, "Invalid rope_mode (must be 0..2)")
+    # 1..3 / 0..2 are the reference's; presets 4..6 and RoPE mode 3 are this
+    # codec's extension kinds (include/ztcp.h)
+    _check(1 <= preset <= 6, "Invalid preset (must be 1..6)")
+    _check(0 <= rope_mode <= 3, "Invalid rope_mode (must be 0..3)")
     th = _hashes_on(page_token_hashes, k_pages.device, "page_token_hashes", B)
     g = N.geometry(T, H, D, rope_dim, dt, False)
     aad = N.Aad(tenant_id_hash & 0xFFFFFFFF, model_id_hash & 0xFFFFFFFF, layer_id & 0xFFFF,
@@ -153,12 +155,14 @@ def fused_decode_cold_pages_peak_into(
     out_v_pages_opt: torch.Tensor | None, rope_dim: int, is_mla_single_buffer: bool,
     expected_tenant_hash: int, expected_model_hash: int, expected_layer_id: int,
     k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0, *,
-    page_status: torch.Tensor | None = None, per_page: bool = False,
+    page_status: torch.Tensor | None = None, per_page: bool = False, ext_layouts: bool = False,
 ) -> None:
     """Batch ingress into preallocated outputs (cpp:2250-2496).
 
     Raises the reference's integrity errors for the lowest failing page; with
-    the default all-or-nothing policy both outputs are zeroed first."""
+    the default all-or-nothing policy both outputs are zeroed first.
+    ``ext_layouts`` accepts the extension presets / RoPE mode in headers
+    (otherwise they fail the flags check, as in the reference)."""
     _check(cold_blobs.is_cuda and cold_blobs.is_contiguous() and cold_blobs.dtype == torch.uint8,
            "cold_blobs must be contiguous HIP uint8")
     _check(cold_blobs.dim() == 2, "cold_blobs must have shape [batch, total_blob_bytes]")
@@ -183,7 +187,7 @@ def fused_decode_cold_pages_peak_into(
                and page_status.is_contiguous(), "page_status must be a contiguous HIP int32 [batch]")
         st_ptr = page_status.data_ptr()
     g = N.geometry(T, H, D, rope_dim, dt, is_mla_single_buffer)
-    flags = N.PER_PAGE if per_page else 0
+    flags = (N.PER_PAGE if per_page else 0) | (N.EXT_LAYOUTS if ext_layouts else 0)
     with torch.cuda.device(cold_blobs.device):
         rc = N.lib().ztcp_ingress_peak_into(
             cold_blobs.data_ptr(), L, th.data_ptr(), out_k_pages.data_ptr(), v_ptr, B, C.byref(g),
@@ -200,7 +204,7 @@ def fused_decode_cold_pages_batch(
     num_heads: int, head_dim: int, rope_dim: int, is_mla_single_buffer: bool,
     expected_tenant_hash: int, expected_model_hash: int, expected_layer_id: int,
     k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0, *,
-    dtype: torch.dtype = torch.float16,
+    dtype: torch.dtype = torch.float16, ext_layouts: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Allocating batch ingress (cpp:2006-2248)."""
     _check(cold_blobs.dim() == 2, "cold_blobs must have shape [batch, total_blob_bytes]")
@@ -209,7 +213,8 @@ def fused_decode_cold_pages_batch(
     v = None if is_mla_single_buffer else torch.empty(shape, dtype=dtype, device=cold_blobs.device)
     fused_decode_cold_pages_peak_into(
         cold_blobs, expected_token_hashes, k, v, rope_dim, is_mla_single_buffer,
-        expected_tenant_hash, expected_model_hash, expected_layer_id, k0, k1, mk0, mk1, k2, k3)
+        expected_tenant_hash, expected_model_hash, expected_layer_id, k0, k1, mk0, mk1, k2, k3,
+        ext_layouts=ext_layouts)
     return k, v
 
 

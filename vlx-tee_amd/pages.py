@@ -66,11 +66,13 @@ def ingress(descs: torch.Tensor, n_pages: int, blob_bytes: int, *, num_tokens: i
             is_mla_single_buffer: bool, expected_tenant_hash: int, expected_model_hash: int,
             k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0,
             page_status: torch.Tensor | None = None, per_page: bool = False,
-            asynchronous: bool = False) -> int:
+            asynchronous: bool = False, ext_layouts: bool = False) -> int:
     """Returns the verdict of the lowest failing page (0 = all verified), or 0
-    when ``asynchronous`` (verdicts then land in ``page_status``)."""
+    when ``asynchronous`` (verdicts then land in ``page_status``).
+    ``ext_layouts`` accepts the extension presets / RoPE mode in headers."""
     g = N.geometry(num_tokens, num_heads, head_dim, rope_dim, _DTYPES[dtype], is_mla_single_buffer)
-    flags = (N.PER_PAGE if per_page else 0) | (N.ASYNC if asynchronous else 0)
+    flags = ((N.PER_PAGE if per_page else 0) | (N.ASYNC if asynchronous else 0)
+             | (N.EXT_LAYOUTS if ext_layouts else 0))
     rc = N.lib().ztcp_ingress_batch(descs.data_ptr(), n_pages, blob_bytes, C.byref(g),
                                     expected_tenant_hash & 0xFFFFFFFF,
                                     expected_model_hash & 0xFFFFFFFF,

@@ -22,12 +22,17 @@ class QuantPreset(enum.IntEnum):
     INT4_SYM = 1
     K8V4_ASYM = 2
     FP8_ONLY = 3
+    # extensions (no counterpart in the reference; include/ztcp.h)
+    K8V4_ASYM_G64 = 4   # K int8 asymmetric per 64 (scale + zero point), V int4 per 32
+    FP8_E4M3 = 5        # K and V OCP e4m3 per 16
+    INT4_SYM_G32 = 6    # K and V int4 per 32
 
 
 class RoPEMode(enum.IntEnum):
     QUANTIZE_ALL = 0
     PRESERVE_FP8 = 1
     PRESERVE_RAW = 2
+    PRESERVE_E4M3 = 3   # extension: RoPE columns as e4m3 per 16
 
 
 def pack_header(preset: int, rope_mode: int, tenant_id_hash: int, model_id_hash: int,
@@ -89,6 +94,26 @@ class ColdPageAAD:
                    rope_mode=RoPEMode(h["rope_mode"] & 0x0F), head_group_id=h["head_group_id"])
 
 
+# Section kind of the K columns after the RoPE ones, and of V, per preset.
+_KMAIN = {1: "int4", 2: "int8", 3: "int8", 4: "asym8_g64", 5: "e4m3", 6: "int4_g32"}
+_VKIND = {1: "int4", 2: "int4", 3: "int8", 4: "int4_g32", 5: "e4m3", 6: "int4_g32"}
+# kind -> (elements per group, code bytes per group, parameter bytes per group)
+_EXT_GROUP = {"e4m3": (16, 16, 2), "int4_g32": (32, 16, 2), "asym8_g64": (64, 64, 4)}
+
+
+def _section_bytes(kind: str, vecs: int, width: int) -> int:
+    if kind == "raw":
+        return vecs * width * 2
+    if kind == "int8":  # the reference's per-column formula (cpp:1450-1472)
+        return vecs * width + vecs * (width // 16) * 2
+    if kind == "int4":
+        return vecs * (width // 2) + vecs * (width // 16) * 2
+    ges, cb, pb = _EXT_GROUP[kind]
+    if width % ges:
+        raise ValueError(f"{kind} needs section widths divisible by {ges}")
+    return vecs * (width // ges) * (cb + pb)
+
+
 @dataclass(frozen=True)
 class ColdPageGeometry:
     num_tokens: int = 64
@@ -121,20 +146,19 @@ class ColdPageGeometry:
         return buffers * self.vectors_per_buffer * self.head_dim * self.hot_element_bytes
 
     def required_payload_bytes(self, preset: int, rope_mode: int) -> int:
-        """Unpadded payload (cpp:1439-1474)."""
-        if preset not in (1, 2, 3) or rope_mode not in (0, 1, 2):
+        """Unpadded payload (cpp:1439-1474; presets 4..6 and RoPE mode 3 are
+        this codec's extension kinds, sized from their group geometry)."""
+        if preset not in (1, 2, 3, 4, 5, 6) or rope_mode not in (0, 1, 2, 3):
             raise ValueError("Invalid preset or rope_mode")
         vecs, D, R = self.vectors_per_buffer, self.head_dim, self.rope_dim
         req = 0
-        if rope_mode == 2 and R > 0:
-            req += vecs * R * 2
-        elif rope_mode == 1 and R > 0:
-            req += vecs * R + vecs * (R // 16) * 2
+        if rope_mode != 0 and R > 0:
+            req += _section_bytes({1: "int8", 2: "raw", 3: "e4m3"}[rope_mode], vecs, R)
         kq = D if rope_mode == 0 else D - R
         if kq > 0:
-            req += (vecs * (kq // 2) if preset == 1 else vecs * kq) + vecs * (kq // 16) * 2
+            req += _section_bytes(_KMAIN[preset], vecs, kq)
         if not self.is_mla_single_buffer:
-            req += (vecs * (D // 2) if preset in (1, 2) else vecs * D) + vecs * (D // 16) * 2
+            req += _section_bytes(_VKIND[preset], vecs, D)
         return req
 
     def payload_bytes(self, preset: int, rope_mode: int) -> int:
