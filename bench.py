@@ -86,7 +86,7 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
     def ingress():
         P.ingress(d_in, w.n_pages, w.blob_bytes, expected_tenant_hash=TENANT_HASH,
                   expected_model_hash=MODEL_HASH, page_status=status, asynchronous=True,
-                  per_page=bool(len(t_pages)), **geo, **keys)
+                  per_page=bool(len(t_pages)), ext_layouts=w.extension, **geo, **keys)
 
     want_status = np.zeros(w.n_pages, dtype=np.int32)
     if len(t_pages):
@@ -252,7 +252,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c2_k8v4_prefix1g")
-    ap.add_argument("--also", default="c2_int4_prefix1g,c3_fp8only_tamper,c4_mla_int4",
+    ap.add_argument("--also", default=("c2_int4_prefix1g,c3_fp8only_tamper,c4_mla_int4,c2_k8v4asym_prefix1g,"
+                                       "c3_e4m3_tamper,c4_mla_int4g32"),
                     help="comma list of extra workloads")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")

@@ -21,6 +21,8 @@ PUBLISHED = {  # (tokens, heads, head_dim, rope, mla) -> [(preset, rope_mode, bl
 CONFIG_BLOBS = {  # the benchmark workloads' blob sizes
     "c0_int4_gqa64": 12336, "c1_int4_gqa256": 12336, "c2_k8v4_prefix1g": 28720,
     "c2_int4_prefix1g": 24624, "c3_fp8only_tamper": 36912, "c4_mla_int4": 25136,
+    # extension kinds: asym8 K + e4m3 RoPE + int4/32 V; e4m3 everywhere; MLA int4/32 + e4m3 RoPE
+    "c2_k8v4asym_prefix1g": 27184, "c3_e4m3_tamper": 36912, "c4_mla_int4g32": 23088,
 }
 
 

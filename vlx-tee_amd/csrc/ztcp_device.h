@@ -790,37 +790,57 @@ __device__ __forceinline__ uint32_t asym8_exact(const uint32_t (&w)[4][8], uint3
     return sb | ((uint32_t)zf << 16);
 }
 
+// Order-preserving signed keys of the two 16-bit floats (fp16 or bf16) of a
+// word: k = b ^ ((b >> 15) & 0x7FFF) per half, so that key order is the
+// floats' order, -0 just below +0, and NaN patterns outside +-inf.  The
+// transform is its own inverse.
+typedef short ztcp_short2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ ztcp_short2 order_keys(uint32_t w) {
+    const ztcp_short2 x = __builtin_bit_cast(ztcp_short2, w);
+    return x ^ ((x >> (short)15) & (short)0x7FFF);
+}
+__device__ __forceinline__ uint32_t key_bits(short k) {
+    return (uint32_t)(uint16_t)(k ^ ((k >> 15) & 0x7FFF));
+}
+template <int DT>
+__device__ __forceinline__ float hot_bits_to_f32(uint32_t b) {
+    if constexpr (DT == kHotBf16) return __uint_as_float(b << 16);
+    else return f16_to_f32(b);
+}
+
 // Fast path (finite elements, a positive finite scale): |v * inv| <= 255 *
 // (1 + 2^-10) (x 1.5 for a subnormal scale), so adding 1.5 * 2^23 rounds
 // v * inv to nearest-even in that same add and the low bits of the sum are
 // rne(v * inv) + 2^22; the zero point is added and the result clamped as
-// integers.  A NaN element turns its sum's exponent bits to all ones; the
-// sums' bits are or-ed together to see it, and such a group takes the exact
-// path (NaN codes are 0 there).  min / max over the elements equal the
-// reference-style compares here: NaN is ignored by both, and a -0 bound
-// gives the same range and zero point as a +0 one.
+// integers.  The group's minimum and maximum come from packed 16-bit keys of
+// the raw elements (two per instruction); a NaN element makes one of them a
+// NaN and the group takes the exact path, as do infinities and a zero or
+// infinite scale.  A -0 minimum gives the same range and zero point as the
+// reference-style compares (which keep +0).
 template <int DT>
 __device__ __forceinline__ uint32_t quant_group64_asym8(const uint32_t (&w)[4][8], uint32_t q[16]) {
-    float lo = 0.0f, hi = 0.0f;
+    ztcp_short2 kmin = {0, 0}, kmax = {0, 0};  // keys of +0: the range always includes 0
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float a = hot_lo<DT>(w[c][i]), b = hot_hi<DT>(w[c][i]);
-            lo = __builtin_fminf(__builtin_fminf(lo, a), b);
-            hi = __builtin_fmaxf(__builtin_fmaxf(hi, a), b);
+            const ztcp_short2 k = order_keys(w[c][i]);
+            kmin = __builtin_elementwise_min(kmin, k);
+            kmax = __builtin_elementwise_max(kmax, k);
         }
     }
+    const float lo = hot_bits_to_f32<DT>(key_bits(kmin.x < kmin.y ? kmin.x : kmin.y));
+    const float hi = hot_bits_to_f32<DT>(key_bits(kmax.x > kmax.y ? kmax.x : kmax.y));
     float range = hi - lo;
     range = range > 1e-6f ? range : 1e-6f;
     const uint32_t sb = f32_to_f16(range / 255.0f);
-    const bool finite = hi < __builtin_inff() && lo > -__builtin_inff();
+    const bool special = !(hi < __builtin_inff()) || !(lo > -__builtin_inff()) || sb == 0u || sb >= 0x7C00u;
+    if (__builtin_expect(special, 0)) return asym8_exact<DT>(w, q);
     const float inv = recip_fast(f16_to_f32(sb));
     float zf = __builtin_rintf(-lo * inv);
     zf = zf < 0.0f ? 0.0f : (zf > 255.0f ? 255.0f : zf);
     const uint32_t z = (uint32_t)zf;
     const uint32_t bias = 0x4B400000u - z;  // bits of 1.5 * 2^23, less the zero point
-    uint32_t seen = 0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
@@ -830,18 +850,12 @@ __device__ __forceinline__ uint32_t quant_group64_asym8(const uint32_t (&w)[4][8
             for (int i = 0; i < 4; ++i) {
                 const uint32_t e = w[c][2 * j + (i >> 1)];
                 const float v = (i & 1) ? hot_hi<DT>(e) : hot_lo<DT>(e);
-                const uint32_t bits = __float_as_uint(v * inv + 12582912.0f);
-                seen |= bits;
-                const int32_t d = (int32_t)(bits - bias);
+                const int32_t d = (int32_t)(__float_as_uint(v * inv + 12582912.0f) - bias);
                 t[i] = (uint32_t)(d < 0 ? 0 : (d > 255 ? 255 : d));  // v_med3_i32
             }
             q[4 * c + j] = pack_low_bytes(t[0], t[1], t[2], t[3]);
         }
     }
-    // non-finite elements (a NaN one turns its sum's exponent bits to all
-    // ones), a zero or an infinite scale: the exact path
-    const bool special = !finite || sb == 0u || sb >= 0x7C00u || (seen >> 23) != 0x96u;
-    if (__builtin_expect(special, 0)) return asym8_exact<DT>(w, q);
     return sb | (z << 16);
 }
 

@@ -59,6 +59,11 @@ class Workload:
     def payload_bytes(self) -> int:
         return self.geometry.payload_bytes(self.preset, self.rope_mode)
 
+    @property
+    def extension(self) -> bool:
+        """Uses the extension presets / RoPE mode (ingress needs ZTCP_EXT_LAYOUTS)."""
+        return self.preset > 3 or self.rope_mode > 2
+
 
 TENANT = "tenant-alpha-bank"
 MODEL = "Qwen/Qwen3.6-35B-A3B"
@@ -82,6 +87,17 @@ WORKLOADS = {
     "c4_mla_int4": Workload("c4_mla_int4", 16384, 64, 1, 576, 64, True, 1, 1, 256, sigma=0.5,
                             rope_sigma=1.0, rope_scale=1.0, outlier_frac=0.02,
                             outlier_scale=16.0),
+    # The same three prefixes with the extension kinds, as the workloads are
+    # specified: K int8 asymmetric per 64 with the RoPE columns in e4m3 and V
+    # int4 per 32 (preset 4 + RoPE mode 3); FP8 e4m3 everywhere with 1% of the
+    # pages tampered (preset 5); MLA latent int4 per 32 with e4m3 RoPE (preset
+    # 6 + RoPE mode 3).
+    "c2_k8v4asym_prefix1g": Workload("c2_k8v4asym_prefix1g", 16384, 16, 8, 128, 64, False, 4, 3, 256),
+    "c3_e4m3_tamper": Workload("c3_e4m3_tamper", 16384, 16, 8, 128, 64, False, 5, 0, 256,
+                               tamper_frac=0.01),
+    "c4_mla_int4g32": Workload("c4_mla_int4g32", 16384, 64, 1, 576, 64, True, 6, 3, 256, sigma=0.5,
+                               rope_sigma=1.0, rope_scale=1.0, outlier_frac=0.02,
+                               outlier_scale=16.0),
 }
 
 
