@@ -313,3 +313,35 @@ def test_batch_paths_vs_oracle(pkg, O, C, S, mla, dtype):
     with pytest.raises(RuntimeError, match="out_blobs_u8 must not alias"):
         aliased = k.view(torch.uint8).reshape(-1)[:blobs.numel()].view(blobs.shape)
         codec.encode_cold_pages_peak_into(k, v, th_t, aliased, TENANT, sess, aad_next)
+
+
+@pytest.mark.parametrize("mla,preset,rope", [(False, 4, 3), (False, 5, 1), (True, 6, 3)])
+def test_codec_class_extension_presets(pkg, O, C, S, mla, preset, rope):
+    """The session-bound codec with the extension presets: batch encode ==
+    oracle; decode needs accept_extension_layouts (otherwise the reference's
+    flags check rejects the page: KVIntegrityError, outputs zeroed)."""
+    geo = _geom(S, mla)
+    ring = C.EphemeralSessionKeyRing(bytes(range(5, 45)))
+    codec = C.NativeCppFusedColdPageCodec(geo, ring, dtype=torch.bfloat16, accept_extension_layouts=True)
+    strict = C.NativeCppFusedColdPageCodec(geo, ring, dtype=torch.bfloat16)
+    B = 4
+    k, v = _pages(geo, B, seed=9, dtype=torch.bfloat16)
+    sess = "sess-ext"
+    aad = S.ColdPageAAD(S.hash32(TENANT), S.hash32(MODEL), LAYER, 0, ring.next_sequence_nonce(TENANT, sess, B),
+                        preset=S.QuantPreset(preset), rope_mode=S.RoPEMode(rope), head_group_id=1)
+    ths = [_i64(S.hash64_tokens(range(64 * i, 64 * i + 64))) for i in range(B)]
+    th_t = torch.tensor(ths, dtype=torch.int64)
+    blobs = codec.encode_cold_pages_batch_tensor(k, v, th_t, TENANT, sess, aad)
+    keys = _session_keys(ring, TENANT, sess)
+    want = _oracle_blobs(O, geo, k, v, ths, aad, keys)
+    assert np.array_equal(blobs.cpu().numpy(), want)
+    rc, _, ok, ov = _oracle_decode(O, geo, want, ths, aad.tenant_id_hash, aad.model_id_hash, LAYER, keys,
+                                   torch.bfloat16)
+    assert rc == 0
+    ko = torch.full_like(k, 3.0)
+    vo = None if mla else torch.full_like(v, 3.0)
+    with pytest.raises(C.KVIntegrityError):
+        strict.decode_cold_pages_peak_into(blobs, th_t, ko, vo, TENANT, sess, MODEL, LAYER)
+    assert not ko.any() and (mla or not vo.any())
+    kd, vd = codec.decode_cold_pages_batch_tensor(blobs, th_t.cuda(), TENANT, sess, MODEL, LAYER)
+    assert np.array_equal(_bits(kd), ok) and (mla or np.array_equal(_bits(vd), ov))

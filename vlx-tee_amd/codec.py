@@ -68,12 +68,17 @@ class NativeHipFusedColdPageCodec:
     session key ring (nfc:68-78)."""
 
     def __init__(self, geometry: ColdPageGeometry, keyring: EphemeralSessionKeyRing,
-                 dtype: torch.dtype = torch.float16) -> None:
+                 dtype: torch.dtype = torch.float16, accept_extension_layouts: bool = False) -> None:
+        """``accept_extension_layouts``: decode pages whose headers carry this
+        codec's extension presets / RoPE mode (QuantPreset 4..6,
+        RoPEMode.PRESERVE_E4M3); by default they fail the flags check as in the
+        reference (KVIntegrityError)."""
         if dtype not in (torch.float16, torch.bfloat16):
             raise ValueError("dtype must be torch.float16 or torch.bfloat16")
         self.geometry = geometry
         self.keyring = keyring
         self.dtype = dtype
+        self.accept_extension_layouts = bool(accept_extension_layouts)
         from . import _native
 
         self._ext = _native.lib()  # fails loudly when the HIP library is missing
@@ -169,7 +174,7 @@ class NativeHipFusedColdPageCodec:
                 cold_blob_u8, g.num_tokens, g.num_kv_heads, g.head_dim, g.rope_dim,
                 g.is_mla_single_buffer, hash32(expected_tenant_id), hash32(expected_model_id),
                 expected_layer_id, expected_token_hash & 0xFFFFFFFFFFFFFFFF,
-                **_keys(enc_key, mac_key), dtype=self.dtype)
+                **_keys(enc_key, mac_key), dtype=self.dtype, ext_layouts=self.accept_extension_layouts)
         except RuntimeError as exc:
             mapped = _map_integrity(exc)
             if mapped is exc:
@@ -200,7 +205,8 @@ class NativeHipFusedColdPageCodec:
                 H.fused_decode_cold_pages_peak_into(
                     cold_blobs_u8, expected_token_hashes_i64, out_k, out_v, self.geometry.rope_dim,
                     self.geometry.is_mla_single_buffer, hash32(expected_tenant_id),
-                    hash32(expected_model_id), expected_layer_id, **keys)
+                    hash32(expected_model_id), expected_layer_id, **keys,
+                    ext_layouts=self.accept_extension_layouts)
             except RuntimeError as exc:
                 mapped = _map_integrity(exc)
                 if mapped is exc:

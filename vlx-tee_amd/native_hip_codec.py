@@ -222,7 +222,7 @@ def fused_decode_cold_page(
     cold_blob: torch.Tensor, num_tokens: int, num_heads: int, head_dim: int, rope_dim: int,
     is_mla_single_buffer: bool, expected_tenant_hash: int, expected_model_hash: int,
     expected_layer_id: int, expected_token_hash: int, k0: int, k1: int, mk0: int, mk1: int,
-    k2: int = 0, k3: int = 0, *, dtype: torch.dtype = torch.float16,
+    k2: int = 0, k3: int = 0, *, dtype: torch.dtype = torch.float16, ext_layouts: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Single-page ingress (cpp:1557-1773)."""
     _check(cold_blob.dim() == 1, "cold_blob must be a 1D tensor")
@@ -232,7 +232,7 @@ def fused_decode_cold_page(
     k, v = fused_decode_cold_pages_batch(
         cold_blob.unsqueeze(0), th, num_tokens, num_heads, head_dim, rope_dim,
         is_mla_single_buffer, expected_tenant_hash, expected_model_hash, expected_layer_id,
-        k0, k1, mk0, mk1, k2, k3, dtype=dtype)
+        k0, k1, mk0, mk1, k2, k3, dtype=dtype, ext_layouts=ext_layouts)
     return k[0], (None if v is None else v[0])
 
 
