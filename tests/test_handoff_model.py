@@ -15,7 +15,9 @@ the model follows the constants the kernels are built with.
     order, stage scales per unit, write the ring at the row's payload
     position; the wave that stages a unit's last code row makes the unit's
     scale row; a feeder copies each stored scale row into the ring at its
-    payload position; the MAC wave absorbs rows in payload order.
+    payload position; the MAC wave absorbs rows in payload order; a storer
+    wave stores every code row from the ring in payload order; a slot is
+    rewritten only once both the MAC wave and the storer have passed it.
   ingress (vlx-tee_amd/csrc/ztcp_ingress.hip): decoders take tasks in order
     (a unit's scale row two units ahead of its code rows), write code rows
     into the ring, stage decrypted scales; a feeder copies every other
@@ -39,6 +41,7 @@ def _const(fname, name):
 
 NBLK = {"i8": 8, "i4": 4, "raw": 16}
 LATE_SCALE_PUBLISH = False  # planted mistake: publish a stored scale row after the row's staging wait
+IGNORE_STORER = False       # planted mistake: reuse a ring slot once the MAC wave alone has passed it
 CONFIGS = {  # sections (kind, units) of the layouts the kernels meet
     "k8v4": [("i8", 16), ("i8", 16), ("i4", 32)],
     "int4": [("i8", 16), ("i4", 16), ("i4", 32)],
@@ -112,8 +115,11 @@ def egress_model(secs, n_prod, seed):
     for c in code:
         if c["quant"]:
             per_unit[c["g"]] = per_unit.get(c["g"], 0) + 1
-    st = dict(task=0, used=0)
+    st = dict(task=0, used=0, stored=0)
     ring, ring_flag = [None] * KRING, [0] * KRING
+
+    def slot_free(m):
+        return st["used"] >= m - KRING + 1 and (IGNORE_STORER or st["stored"] >= m - KRING + 1)
     stage_flag, count = [0] * KSTAGE, [0] * KSTAGE
     stage_units = [None] * KSTAGE
     staged, stored = {}, set()
@@ -150,7 +156,7 @@ def egress_model(secs, n_prod, seed):
                 stored.add(owed)
                 yield "ok"
             m = c["m"]
-            yield from wait(lambda: st["used"] >= m - KRING + 1)
+            yield from wait(lambda: slot_free(m))
             assert ring_flag[m % KRING] <= max(0, m - KRING + 1), "ring slot overwritten before use"
             ring[m % KRING] = prow[m]
             yield "ok"
@@ -181,7 +187,7 @@ def egress_model(secs, n_prod, seed):
             if i + 1 < len(rows) and rows[i + 1][0] == m + 1:
                 gn = rows[i + 1][1]
                 yield from wait(lambda: gn in stored)
-            yield from wait(lambda: st["used"] >= m - KRING + 1)
+            yield from wait(lambda: slot_free(m))
             assert ring_flag[m % KRING] <= max(0, m - KRING + 1)
             ring[m % KRING] = prow[m]
             yield "ok"
@@ -195,7 +201,16 @@ def egress_model(secs, n_prod, seed):
             st["used"] = m + 1
             yield "ok"
 
-    return Sched(seed).run([producer() for _ in range(n_prod)] + [feeder(), mac()])
+    def storer():  # code rows only; scale rows are stored by their makers
+        for m in range(len(prow)):
+            if prow[m][0] == "code":
+                yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
+                yield "ok"  # the slot's quads are read ...
+                assert ring[m % KRING] == prow[m], ("storer read an overwritten slot", m, ring[m % KRING])
+            st["stored"] = m + 1  # ... before the release that frees it
+            yield "ok"
+
+    return Sched(seed).run([producer() for _ in range(n_prod)] + [feeder(), mac(), storer()])
 
 
 def ingress_tasks(secs, L):
@@ -234,8 +249,11 @@ def ingress_model(secs, n_dec, seed, padding=0):
     tasks = ingress_tasks(secs, L)
     code_m = {t["m"] for t in tasks if t["kind"] == "code"}
     assert len(code_m) == sum(1 for r in prow if r[0] == "code")
-    st = dict(task=0, used=0)
+    st = dict(task=0, used=0, stored=0)
     ring, ring_flag = [None] * KRING, [0] * KRING
+
+    def slot_free(m):
+        return st["used"] >= m - KRING + 1 and (IGNORE_STORER or st["stored"] >= m - KRING + 1)
     ready, free, count = [0] * KSTAGE, [0] * KSTAGE, [0] * KSTAGE
     stage = [None] * KSTAGE
 
@@ -319,6 +337,19 @@ def test_egress_model_catches_a_late_scale_publication():
         assert not all(egress_model(CONFIGS["k8v4"], 48, seed) for seed in range(5))
     finally:
         LATE_SCALE_PUBLISH = False
+
+
+def test_egress_model_catches_a_slot_reused_before_the_storer_read_it():
+    """A planted mistake: producers that reuse a ring slot as soon as the MAC
+    wave has passed it can overwrite a row the storer has not stored yet."""
+    global IGNORE_STORER
+    IGNORE_STORER = True
+    try:
+        with pytest.raises(AssertionError, match="storer read an overwritten slot"):
+            for seed in range(20):
+                egress_model(CONFIGS["fp8only"], 48, seed)
+    finally:
+        IGNORE_STORER = False
 
 
 def test_model_catches_a_staging_ring_smaller_than_the_lookahead():

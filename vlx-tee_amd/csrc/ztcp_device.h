@@ -269,6 +269,27 @@ struct Sip {
         }
         absorb_words<8>(w);
     }
+    // absorb64 with after_word(i) called after word i (i = 0..7), so that a
+    // caller can spread other work (memory instructions) over the chain.
+    template <class F>
+    __device__ __forceinline__ void absorb64_with(const uint4 (&c)[4], F&& after_word) {
+        uint64_t w[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[2 * i] = (uint64_t)c[i].x | ((uint64_t)c[i].y << 32);
+            w[2 * i + 1] = (uint64_t)c[i].z | ((uint64_t)c[i].w << 32);
+        }
+        v3 ^= w[0];
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            compress_then_inject(w[i], w[i + 1]);
+            after_word(i);
+        }
+        round();
+        round();
+        v0 ^= w[7];
+        after_word(7);
+    }
     // Final word = (total_len & 0xff) << 56 | tail bytes (cpp:458-470), then
     // the 128-bit finalization (cpp:447-456).
     __device__ __forceinline__ void finish(uint64_t last_word, uint64_t& lo, uint64_t& hi) {

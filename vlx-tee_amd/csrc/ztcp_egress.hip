@@ -10,15 +10,20 @@
 //     pages of the workgroup.  Every payload block is exactly one row: a code
 //     row (4 int8 / e4m3 / int4-per-32 groups, 8 int4 groups, 2 raw groups
 //     or 1 asym8 group) or a scale row (the 64 parameter bytes of one unit).
-//   * Twelve producer waves (on SIMDs 1-3) take code rows in order from an
+//   * Eleven producer waves (on SIMDs 1-3) take code rows in order from an
 //     LDS counter.  A code row quantizes its groups (loaded a row ahead),
 //     stages the scales in LDS, computes the keystream, XORs, and writes the
 //     ciphertext into a ring of row slots in LDS at its place in payload
-//     order.  From the slot it stores the row to the blobs transposed: four
-//     lanes per page, 64 contiguous bytes per page per store.  The wave that
-//     stages a unit's last scales (an LDS counter per staging slot) also
-//     makes the unit's scale row during its next code row: it encrypts the
-//     staged scales and stores them the same way.
+//     order.  The wave that stages a unit's last scales (an LDS counter per
+//     staging slot) also makes the unit's scale row during its next code
+//     row: it encrypts the staged scales and stores them to the blobs,
+//     transposed (four lanes per page, 64 contiguous bytes per page per
+//     store).
+//   * A storer wave (wave 1, SIMD 1) stores every code row from the ring to
+//     the blobs the same transposed way, in payload order.  Producers issue
+//     no code-row stores: a wave's wait for its own loads also waits for
+//     every store it issued before them, which exposed the int4 rows' second
+//     loads; and the MAC wave's SIMD is kept free of stores.
 //   * Wave 0 runs SipHash for one page per lane, at raised priority on SIMD
 //     0.  It absorbs the header, then the payload rows in order from the
 //     ring, so it never reads global memory.  Scale rows reach the ring
@@ -29,7 +34,8 @@
 //     MAC chain down more than they add.
 //   * Hand-offs are monotonic LDS counters with workgroup-scope
 //     release/acquire: ring_flag[slot] = payload row index + 1 when written,
-//     mac_used = rows absorbed (frees ring slots), stage_flag[slot] = unit + 1
+//     mac_used = rows absorbed and stored = rows stored (a slot is free once
+//     both have passed it), stage_flag[slot] = unit + 1
 //     when a scale row has read its staging slot, scale_flag[slot] = unit + 1
 //     once the scale row's stores have completed.  Every wait is bounded; an
 //     expired wait sets a sticky diagnostic bit and the kernel still ends.
@@ -46,7 +52,8 @@ namespace {
 
 // 16 waves, four per SIMD: the MAC wave (0) and the scale-row feeder (4) on
 // SIMD 0 (waves 8 and 12 exit at once: producers there slow the MAC chain
-// down more than they add), twelve producers on the other three SIMDs.
+// down more than they add), the storer (1) and eleven producers on the other
+// three SIMDs.
 // 128 VGPRs each.
 constexpr int kEgressWaves = 16;
 constexpr int kEgressThreads = 64 * kEgressWaves;
@@ -60,7 +67,8 @@ constexpr int kFlagStage = kFlagRing + kRing;         // [kStage] unit + 1: stag
 constexpr int kFlagCount = kFlagStage + kStage;       // [kStage] code rows staged in the slot
 constexpr int kFlagScale = kFlagCount + kStage;       // [kScaleSlots] unit + 1: scale row stored
 constexpr int kFlagMacUsed = kFlagScale + kScaleSlots;  // rows absorbed by the MAC wave
-constexpr int kFlagTask = kFlagMacUsed + 1;           // next code row to hand out
+constexpr int kFlagStored = kFlagMacUsed + 1;         // rows passed by the storer wave
+constexpr int kFlagTask = kFlagStored + 1;            // next code row to hand out
 constexpr int kNumFlags = (kFlagTask + 2) & ~1;  // even: the blob table after it is 8-byte aligned
 constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byte aligned)
 constexpr int kLdsWords = kLdsBlobs + 2 * 64;
@@ -315,13 +323,13 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
     uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
     wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, p.state);
+    wait_ge<kDiagEgressWait>(&flags[kFlagStored], row.mrow - kRing + 1, p.state);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad(slot, c.lane, q,
                      make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
                                 pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
-    store_row(slot, c, (uint32_t)kHeader + 64u * (uint32_t)row.block);
-    publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);
+    publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);  // the storer wave stores it
 }
 
 template <int DT, int FAM>
@@ -445,7 +453,7 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     DeviceState* st = p.state;
     __builtin_amdgcn_s_waitcnt(0);
     mac_rows<kRing, kDiagEgressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
-                                     m.total);
+                                     m.total, [](int32_t, int, const uint4&) {});
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     if (active)
@@ -478,6 +486,7 @@ __device__ __forceinline__ void feed_put(const EgressParams& p, uint32_t* lds, c
                                          const uint4 (&x)[4]) {
     uint32_t* flags = lds + kLdsFlags;
     wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], rs - kRing + 1, p.state);
+    wait_ge<kDiagEgressWait>(&flags[kFlagStored], rs - kRing + 1, p.state);
     uint32_t* slot = lds + (rs % kRing) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
@@ -516,6 +525,38 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
 // FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also the
 // extension kinds (e4m3, int4 per 32, asym8).  Separate instantiations keep
 // the extension's registers out of the reference kinds' kernel.
+// Storer (one wave on SIMD 1): stores every code row from the ring to the
+// blobs, in payload order (the MAC order), transposed -- four lanes per page,
+// 64 contiguous bytes of 16 pages per store instruction -- and publishes
+// `stored` = rows passed; a ring slot is rewritten only once the MAC wave and
+// the storer have both passed it.  Scale rows are skipped: their makers store
+// them.  Stores are kept off the producers, whose waits for their own loads
+// would otherwise also wait for every store they issued before those loads,
+// and off the MAC wave's SIMD, where the data and address reads of scattered
+// stores take register-file cycles from the chain.  The storer issues no
+// loads, so it never waits for its stores.
+__device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
+    ProducerCtx c;
+    c.p = &p;
+    c.lane = threadIdx.x & 63;
+    c.lds = lds;
+    c.init_stores(ppw);
+    MacPlan m;
+    m.init(p.lay);
+    const int32_t s0 = m.nc0, s1 = m.nc0 + m.ns0 + m.nc1, s2 = s1 + m.ns1 + m.nc2;  // first scale row of each section
+    uint32_t* flags = lds + kLdsFlags;
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll 1
+    for (int32_t r = 0; r < m.total; ++r) {
+        const bool scale = (r >= s0 && r < s0 + m.ns0) || (r >= s1 && r < s1 + m.ns1) || (r >= s2 && r < s2 + m.ns2);
+        if (!scale) {
+            wait_ge<kDiagEgressWait>(&flags[kFlagRing + r % kRing], r + 1, p.state);
+            store_row(lds + (r % kRing) * kRowWords, c, (uint32_t)kHeader + 64u * (uint32_t)r);
+        }
+        publish(&flags[kFlagStored], (uint32_t)r + 1u);  // the release orders the slot reads before it
+    }
+}
+
 template <int DT, int FAM>
 __global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
@@ -539,6 +580,10 @@ __global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressPara
         return;
     }
     if ((wave & 3) == 0) return;  // the rest of the MAC wave's SIMD stays idle
+    if (wave == 1) {
+        egress_store_rows(p, page0, ppw, lds);
+        return;
+    }
     egress_produce<DT, FAM>(p, page0, ppw, lds);
 }
 

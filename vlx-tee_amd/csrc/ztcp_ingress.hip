@@ -681,7 +681,7 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     DeviceState* st = p.state;
     __builtin_amdgcn_s_waitcnt(0);
     mac_rows<kRing, kDiagIngressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
-                                      total);
+                                      total, [](int32_t, int, const uint4&) {});
 #pragma unroll
     for (int i = 0; i < 3; ++i)
         if (i < ntail) s.absorb(tl[i]);

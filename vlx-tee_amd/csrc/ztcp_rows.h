@@ -97,18 +97,23 @@ __device__ __forceinline__ void mac_fetch(const uint32_t* ring, const uint32_t* 
 
 // Absorbs payload row `want - 1` and releases its slot.  `ready` says
 // whether the row's flag read already showed the row; otherwise the row is
-// read again once the flag is set.
-template <uint32_t DIAG>
+// read again once the flag is set.  The previous row's quads (in `prev`, when
+// has_prev) go to on_quad(row, q, quad) one at a time after words 0, 2, 4, 6
+// of this row: memory instructions spread over the chain cost it nothing,
+// while four in a row stall the wave on the address unit.
+template <uint32_t DIAG, class OnQuad>
 __device__ __forceinline__ void mac_absorb(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
                                            uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want,
-                                           bool ready) {
+                                           bool ready, OnQuad& on_quad, const MacRow& prev, bool has_prev) {
     if (!ready) {
         wait_ge<DIAG>(ring_flags + r.slot, want, st);
 #pragma unroll
         for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
     }
-    s.absorb64(r.x);
+    s.absorb64_with(r.x, [&](int i) {
+        if ((i & 1) == 0 && has_prev) on_quad(want - 2, i >> 1, prev.x[i >> 1]);
+    });
     publish(used, (uint32_t)want);
 }
 
@@ -116,38 +121,51 @@ __device__ __forceinline__ bool mac_ready(const MacRow& r, int32_t want) {
     return (int32_t)__builtin_amdgcn_readfirstlane(r.f) >= want;
 }
 
-// Absorbs payload rows [0, total) from a ring of RING slots.  Two rows are
-// in flight; a row is fetched right after the absorption that frees its
-// registers, so every read has a whole row's absorption to complete before
-// it is used and no wait lands on a fresh read.  A row's ready flag is
-// tested right after the previous row's slot is released (a release waits
-// for every LDS operation issued before it, so the flag value is there
+// Absorbs payload rows [0, total) from a ring of RING slots.  Three row
+// buffers rotate: two rows are in flight while one is absorbed, and a buffer
+// is fetched again one absorption after the one that read it, so every read
+// has a whole row's absorption to complete before it is used and no wait
+// lands on a fresh read; a row's quads go to on_quad during the next row's
+// absorption, from the buffer that still holds it.  A row's ready
+// flag is tested right after the previous row's slot is released (a release
+// waits for every LDS operation issued before it, so the flag value is there
 // already), never at the loop head, where the wait would also cover the
-// fetch just issued.  Fetches are unconditional (past the last row they
-// read slots that are never absorbed): a fetch under a branch would leave
-// the buffer in different registers on the two paths, and the copy that
-// joins them would wait for the fresh read.  The caller completes every
-// load it has issued before the call: a load still counted as in flight
-// where the loop begins (a scalar load in particular, as those complete out
-// of order) would turn the loop's LDS waits into full waits.
-template <int RING, uint32_t DIAG>
+// fetch just issued.  Fetches are unconditional (past the last row they read
+// slots that are never absorbed): a fetch under a branch would leave the
+// buffer in different registers on the two paths, and the copy that joins
+// them would wait for the fresh read.  The caller completes every load it
+// has issued before the call: a load still counted as in flight where the
+// loop begins (a scalar load in particular, as those complete out of order)
+// would turn the loop's LDS waits into full waits.
+template <int RING, uint32_t DIAG, class OnQuad>
 __device__ __forceinline__ void mac_rows(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
-                                         uint32_t* used, const PageQuads& pq, Sip& s, int32_t total) {
-    MacRow r0, r1;
+                                         uint32_t* used, const PageQuads& pq, Sip& s, int32_t total,
+                                         OnQuad&& on_quad) {
+    MacRow r0, r1, r2;
     int32_t slot = 0;
     auto next_slot = [&]() { const int32_t v = slot; slot = slot == RING - 1 ? 0 : slot + 1; return v; };
+    // the last absorbed row's quads, once no row follows to carry them
+    auto flush = [&](const MacRow& r, int32_t row) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) on_quad(row, q, r.x[q]);
+    };
     mac_fetch(ring, ring_flags, pq, next_slot(), r0);
     mac_fetch(ring, ring_flags, pq, next_slot(), r1);
     bool ok0 = mac_ready(r0, 1);
 #pragma unroll 1
-    for (int32_t c = 0; c < total; c += 2) {
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r0, c + 1, ok0);
+    for (int32_t c = 0; c < total; c += 3) {
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r0, c + 1, ok0, on_quad, r2, c > 0);
         const bool ok1 = mac_ready(r1, c + 2);
+        mac_fetch(ring, ring_flags, pq, next_slot(), r2);
+        if (c + 1 >= total) { flush(r0, c); break; }
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r1, c + 2, ok1, on_quad, r0, true);
+        const bool ok2 = mac_ready(r2, c + 3);
         mac_fetch(ring, ring_flags, pq, next_slot(), r0);
-        if (c + 1 >= total) break;
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r1, c + 2, ok1);
-        ok0 = mac_ready(r0, c + 3);
+        if (c + 2 >= total) { flush(r1, c + 1); break; }
+        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r2, c + 3, ok2, on_quad, r1, true);
+        ok0 = mac_ready(r0, c + 4);
         mac_fetch(ring, ring_flags, pq, next_slot(), r1);
+        if (c + 3 >= total) { flush(r2, c + 2); break; }
     }
 }
 
