@@ -365,11 +365,19 @@ __device__ __forceinline__ float hot_hi(uint32_t w) {  // element in bits 16..31
     if constexpr (DT == kHotBf16) return __uint_as_float(w & 0xFFFF0000u);
     else return f16_to_f32(w >> 16);
 }
-// Two fp32 values -> packed hot pair (lo in bits 0..15), RNE.
+// Two fp32 values -> packed hot pair (lo in bits 0..15), RNE.  The bf16 pair
+// goes through one two-wide conversion (a single v_cvt_pk_bf16_f32); two
+// scalar conversions cost a conversion, a shift and an or per element.
+typedef float ztcp_float2 __attribute__((ext_vector_type(2)));
+typedef __bf16 ztcp_bf16x2 __attribute__((ext_vector_type(2)));
 template <int DT>
 __device__ __forceinline__ uint32_t pack_hot(float lo, float hi) {
-    if constexpr (DT == kHotBf16) return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-    else return f32_to_f16(lo) | (f32_to_f16(hi) << 16);
+    if constexpr (DT == kHotBf16) {
+        const ztcp_float2 f = {lo, hi};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, ztcp_bf16x2));
+    } else {
+        return f32_to_f16(lo) | (f32_to_f16(hi) << 16);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -598,12 +606,14 @@ __device__ __forceinline__ void dequant_group_int4(const uint32_t q[2], uint32_t
     const float s = f16_to_f32(scale_bits & 0xFFFFu);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const uint32_t lo = q[j] & 0x0F0F0F0Fu;         // elements 0,2,4,6 of the word
-        const uint32_t hi = (q[j] >> 4) & 0x0F0F0F0Fu;  // elements 1,3,5,7
+        // nibble n ^ 8 is n - 8 in 4-bit two's complement: a signed field
+        // extract gives the code's value in one instruction
+        const int32_t x = (int32_t)(q[j] ^ 0x88888888u);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float a = ((float)((lo >> (8 * i)) & 0xFFu) - 8.0f) * s;
-            float b = ((float)((hi >> (8 * i)) & 0xFFu) - 8.0f) * s;
+            // (the builtin's result type is unsigned: the value is read as int32_t)
+            const float a = (float)(int32_t)__builtin_amdgcn_sbfe(x, 8u * i, 4u) * s;       // element 2i
+            const float b = (float)(int32_t)__builtin_amdgcn_sbfe(x, 8u * i + 4u, 4u) * s;  // element 2i + 1
             out[4 * j + i] = pack_hot<DT>(a, b);
         }
     }
