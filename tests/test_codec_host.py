@@ -3,6 +3,7 @@ instead of a kernel (no GPU): the reference's ordering of nonce burn,
 argument checks, output zeroing and session errors (nfc:148-606)."""
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -76,3 +77,18 @@ def test_reference_names_are_exported(C):
     assert issubclass(C.CrossTenantContaminationError, C.KVIntegrityError)
     assert issubclass(C.NonceReuseError, ValueError)
     assert issubclass(C.SessionShreddedError, RuntimeError)
+
+
+def test_hit_bitmap_packing(pkg):
+    """Packed hit bitmap against numpy's little-endian bit packing."""
+    import vlx_tee_amd.serving as SV
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 7, 8, 9, 1000):
+        st = rng.choice(np.array([0, 0, 0, 1, 2, 3], dtype=np.int32), size=n)
+        t = torch.from_numpy(st)
+        hits = SV.hit_bitmap(t)
+        assert hits.dtype == torch.bool and np.array_equal(hits.numpy(), st == 0)
+        packed = SV.hit_bitmap(t, packed=True).numpy()
+        assert np.array_equal(packed, np.packbits(st == 0, bitorder="little"))
+    with pytest.raises(ValueError):
+        SV.hit_bitmap(torch.zeros(4, dtype=torch.int64))

@@ -142,6 +142,10 @@ def test_fp8only_tamper_stress_full_prefix(pkg, O, W):
     want = np.zeros(w.n_pages, dtype=np.int32)
     want[pages] = [_expected_verdict(int(b) // 8) for b in bits]
     assert np.array_equal(st, want)
+    # PoisonShield hit bitmap: False exactly at the tampered slots
+    import vlx_tee_amd.serving as SV
+    hits = SV.hit_bitmap(torch.from_numpy(st).to(blobs.device)).cpu().numpy()
+    assert hits.sum() == w.n_pages - len(pages) and not hits[pages].any()
     assert rc == int(want[pages[0]])  # the lowest failing page's verdict
     # tampered pages zeroed, every other page exactly as without tampering
     ko_clean[idx] = 0
@@ -165,3 +169,31 @@ def test_fp8only_tamper_stress_full_prefix(pkg, O, W):
     clean = np.setdiff1d(np.arange(w.n_pages), pages)
     _sample_vs_oracle(O, W, w, keys, k, v, blobs, ko, vo, th, seq, layers,
                       np.sort(np.random.default_rng(3).choice(clean, size=SAMPLE, replace=False)))
+
+
+def test_wire_ring_egress_copy(pkg, W):
+    """The egress wire step: a full prefix's blobs leave HBM through a ring of
+    two pinned host slots, a quarter of the pages per push, byte for byte."""
+    import time
+    import vlx_tee_amd.serving as SV
+    print("case c2_k8v4_prefix1g: encode for the wire ring", flush=True)
+    w, keys, k, v, th, seq, layers, blobs, geo = _encode(pkg, W, "c2_k8v4_prefix1g")
+    del k, v
+    torch.cuda.synchronize()
+    q = w.n_pages // 4
+    ring = SV.WireRing(q * w.blob_bytes, n_slots=2)
+    host = blobs.cpu()
+    t0 = time.perf_counter()
+    got = []
+    for part in range(4):
+        slot = ring.push(blobs[part * q:(part + 1) * q])
+        if part >= 1:
+            got.append(ring.wait((slot + 1) % 2).clone())
+    got.append(ring.wait(slot).clone())
+    dt = time.perf_counter() - t0
+    print(f"wire ring: {blobs.numel() / dt / 1e9:.1f} GB/s device-to-pinned-host "
+          f"({blobs.numel()} blob bytes, 4 pushes)", flush=True)
+    for part in range(4):
+        assert torch.equal(got[part], host[part * q:(part + 1) * q].reshape(-1))
+    with pytest.raises(ValueError):
+        ring.push(blobs)  # larger than a slot

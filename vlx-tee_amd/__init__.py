@@ -8,12 +8,14 @@ Modules:
   keyring           session key ring, drop-in for EphemeralSessionKeyRing
                     (research/baseline_codec/fused_quant_crypto.py:99-659), native state
   pages             descriptor-based batch API for paged, multi-layer KV pools
+  serving           PoisonShield hit bitmap from per-page verdicts, pinned host ring
+                    for the egress wire step
   spec              wire constants, AAD record and payload sizing (cold_page_spec.py mirror)
   workloads         synthetic page generators for the benchmark configurations
 """
 from . import spec  # noqa: F401
 
-__all__ = ["spec", "native_hip_codec", "codec", "keyring", "pages", "workloads", "load_native"]
+__all__ = ["spec", "native_hip_codec", "codec", "keyring", "pages", "serving", "workloads", "load_native"]
 
 
 def load_native():
