@@ -81,7 +81,7 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
     def egress():
         P.egress(d_out, w.n_pages, preset=w.preset, rope_mode=w.rope_mode,
                  expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
-                 model_id_hash=MODEL_HASH, **geo, **keys)
+                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, **geo, **keys)
 
     def ingress():
         P.ingress(d_in, w.n_pages, w.blob_bytes, expected_tenant_hash=TENANT_HASH,

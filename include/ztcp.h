@@ -21,6 +21,15 @@
  *    Egress returns once enqueued.  Ingress without ZTCP_ASYNC synchronizes
  *    the stream and returns the reference's verdict; with ZTCP_ASYNC it
  *    returns after enqueueing and the verdict is read from `page_status`.
+ *  - Calls may overlap freely (several streams, several host threads): each
+ *    ingress call keeps its failure record in device state of its own, which
+ *    the call holds until its work on the stream has completed.
+ *  - Fail closed: the fused kernels' hand-offs use bounded waits.  If one
+ *    expires (a device-side fault, never expected), ingress fails every page
+ *    of the affected workgroup with ZTCP_ERR_DEVICE and zeroes its outputs, and
+ *    a synchronous ingress returns ZTCP_EDEVICE; egress writes the affected
+ *    workgroup's blobs with a zero header magic, which every ingress rejects
+ *    (status 1).  Either way ztcp_device_diag reports it.
  *  - Keys are passed by value and never retained (nfc:173-174 unpacks them
  *    into the same little-endian u64 words).
  *  - Errors are return codes, never exceptions: negative = argument / runtime
@@ -66,19 +75,25 @@ enum { ZTCP_HOT_FP16 = 0, ZTCP_HOT_BF16 = 1 };
 #define ZTCP_ERR_HEADER 1  /* KV_INTEGRITY_ERROR: magic, version, flags or size */
 #define ZTCP_ERR_AAD 2     /* CROSS_TENANT_CONTAMINATION: tenant/model/layer/token */
 #define ZTCP_ERR_MAC 3     /* KV_INTEGRITY_ERROR: MAC verification failed */
+/* Per-page status only (no counterpart in the reference): the page's
+ * workgroup hit an expired bounded wait; the page is rejected and zeroed. */
+#define ZTCP_ERR_DEVICE 4
 /* Argument / runtime errors. */
 #define ZTCP_EINVAL (-1)   /* a TORCH_CHECK of the reference would fail */
 #define ZTCP_EOVERLAP (-2) /* an output aliases an input (cpp:1428-1437) */
 #define ZTCP_EHIP (-3)     /* the HIP runtime reported an error */
-#define ZTCP_EDEVICE (-4)  /* a kernel's bounded wait expired (see ztcp_device_diag) */
+#define ZTCP_EDEVICE (-4)  /* a kernel's bounded wait expired: outputs are zeroed
+                              (see ztcp_device_diag) */
 
-/* Ingress flags. */
-#define ZTCP_ASYNC 0x1u          /* enqueue only; verdicts land in page_status */
-#define ZTCP_PER_PAGE 0x2u       /* extension: keep verified pages, zero failing ones;
-                                    default is the reference's all-or-nothing */
-#define ZTCP_EXT_LAYOUTS 0x4u    /* extension: accept the extension presets / RoPE
-                                    mode in headers; without it they fail with
-                                    status 1, as the reference's flags check does */
+/* Call flags. */
+#define ZTCP_ASYNC 0x1u          /* ingress: enqueue only; verdicts land in page_status */
+#define ZTCP_PER_PAGE 0x2u       /* ingress extension: keep verified pages, zero failing
+                                    ones; default is the reference's all-or-nothing */
+#define ZTCP_EXT_LAYOUTS 0x4u    /* extension: the extension presets / RoPE mode.  Ingress
+                                    without it fails such headers with status 1, egress
+                                    (the *_ext entry points) without it rejects them with
+                                    ZTCP_EINVAL, as the reference's flags check does
+                                    (cpp:1447-1449) */
 
 typedef struct ztcp_geometry {
     int64_t num_tokens;   /* tokens per page */
@@ -137,22 +152,33 @@ size_t ztcp_blob_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode
 /* Batch egress into a preallocated [batch, 32 + expected_payload_bytes + 16]
  * buffer.  Replaces fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004):
  * page b is read at b * T*H*D elements, encoded with token_hashes[b] and
- * sequence_nonce = base_sequence_nonce + b, and written at b * blob_bytes. */
+ * sequence_nonce = base_sequence_nonce + b, and written at b * blob_bytes.
+ * Presets 1..3 and RoPE modes 0..2, as the reference (cpp:1947-1948). */
 int ztcp_egress_peak_into(const void* k_pages, const void* v_pages,
                           const int64_t* page_token_hashes, uint8_t* out_blobs,
                           int64_t batch, const ztcp_geometry* g, int64_t preset,
                           int64_t rope_mode, int64_t expected_payload_bytes,
                           const ztcp_aad* aad, uint64_t base_sequence_nonce,
                           const ztcp_keys* keys, void* stream);
+/* The same with call flags: ZTCP_EXT_LAYOUTS admits the extension presets
+ * 4..6 and RoPE mode 3 (no counterpart in the reference). */
+int ztcp_egress_peak_into_ext(const void* k_pages, const void* v_pages,
+                              const int64_t* page_token_hashes, uint8_t* out_blobs,
+                              int64_t batch, const ztcp_geometry* g, int64_t preset,
+                              int64_t rope_mode, int64_t expected_payload_bytes,
+                              const ztcp_aad* aad, uint64_t base_sequence_nonce,
+                              const ztcp_keys* keys, uint32_t flags, void* stream);
 
 /* Descriptor form of the same egress for paged, multi-layer KV pools:
  * `pages` is a DEVICE array of n_pages descriptors; tenant and model hashes
  * come from `tenant_id_hash` / `model_id_hash`, every other header field from
- * the page's descriptor.  Same encoding as ztcp_egress_peak_into. */
+ * the page's descriptor.  Same encoding as ztcp_egress_peak_into; `flags`:
+ * ZTCP_EXT_LAYOUTS admits the extension presets / RoPE mode. */
 int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages,
                       const ztcp_geometry* g, int64_t preset, int64_t rope_mode,
                       int64_t expected_payload_bytes, uint32_t tenant_id_hash,
-                      uint32_t model_id_hash, const ztcp_keys* keys, void* stream);
+                      uint32_t model_id_hash, const ztcp_keys* keys, uint32_t flags,
+                      void* stream);
 
 /* Batch ingress into preallocated outputs.  Replaces
  * fused_decode_cold_pages_peak_into_cpu (cpp:2250-2496): every page is
@@ -160,8 +186,9 @@ int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages,
  * token hash -> 2, SipHash tag -> 3, flags/size -> 1), decrypted and
  * dequantized according to its own header flags.  Default (all-or-nothing):
  * if any page fails, both outputs are zeroed and the verdict of the lowest
- * failing page is returned.  page_status (DEVICE int32[batch], may be NULL)
- * receives every page's verdict. */
+ * failing page is returned (ZTCP_EDEVICE when a bounded wait expired).
+ * page_status (DEVICE int32[batch], may be NULL) receives every page's
+ * verdict (0..4). */
 int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
                            const int64_t* expected_token_hashes, void* out_k_pages,
                            void* out_v_pages, int64_t batch, const ztcp_geometry* g,
@@ -201,8 +228,21 @@ int ztcp_selftest(void);
  * sticky flags a kernel's bounded waits set (0 = none). Synchronizes. */
 int ztcp_device_diag(void);
 
+/* Test hook for the fail-closed paths (no counterpart in the reference):
+ * sets the number of polls after which the fused kernels' bounded waits give
+ * up, for calls made afterwards in this process; n < 0 restores the default
+ * (about 30 ms).  n = 0 makes every wait that is not already satisfied expire
+ * at once, so a test can drive the expiry handling to completion without a
+ * fault.  Returns the previous value. */
+int64_t ztcp_debug_spin_limit(int64_t n);
+
 /* Short description of a return code. */
 const char* ztcp_strerror(int code);
+
+/* Why the calling thread's last call returned ZTCP_EINVAL or ZTCP_EOVERLAP:
+ * the reference's TORCH_CHECK message for the same condition where it has
+ * one ("" when the last call succeeded). */
+const char* ztcp_last_error(void);
 
 #ifdef __cplusplus
 }

@@ -49,7 +49,8 @@ def _egress(H, O, k, v, th, preset, rm, R):
     out = torch.full((B, 48 + exp), 0xA5, dtype=torch.uint8, device=dev)
     H.fused_encode_cold_pages_peak_into(k.to(dev), None if v is None else v.to(dev), torch.from_numpy(th),
                                         out, preset, rm, R, exp, TEN, MOD, LAYER, HG, BASE, KEYS["k0"],
-                                        KEYS["k1"], KEYS["mk0"], KEYS["mk1"], KEYS["k2"], KEYS["k3"])
+                                        KEYS["k1"], KEYS["mk0"], KEYS["mk1"], KEYS["k2"], KEYS["k3"],
+                                        ext_layouts=True)
     torch.cuda.synchronize()
     want = O.egress_batch(_bits(k), _bits(v), th, dtype=_odt(O, k.dtype), preset=preset, rope_mode=rm,
                           rope_dim=R, expected_payload_bytes=exp, tenant_id_hash=TEN, model_id_hash=MOD,
@@ -146,7 +147,7 @@ def test_ext_mixed_layouts_in_one_batch(hip, O, dtype):
         hip.fused_encode_cold_pages_peak_into(k[sl].to(dev), v[sl].to(dev), torch.from_numpy(th[sl]), out,
                                               preset, rm, R, width - 48, TEN, MOD, LAYER, HG, BASE + 2 * i,
                                               KEYS["k0"], KEYS["k1"], KEYS["mk0"], KEYS["mk1"], KEYS["k2"],
-                                              KEYS["k3"])
+                                              KEYS["k3"], ext_layouts=True)
         torch.cuda.synchronize()
         blobs[sl] = out.cpu().numpy()
         want = O.egress_batch(_bits(k[sl]), _bits(v[sl]), th[sl], dtype=_odt(O, k.dtype), preset=preset,

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 LIB_PATH = Path(__file__).resolve().parent / "libztcp_hip.so"
 
 # Return codes (include/ztcp.h).
-OK, ERR_HEADER, ERR_AAD, ERR_MAC = 0, 1, 2, 3
+OK, ERR_HEADER, ERR_AAD, ERR_MAC, ERR_DEVICE = 0, 1, 2, 3, 4
 EINVAL, EOVERLAP, EHIP, EDEVICE = -1, -2, -3, -4
 ASYNC, PER_PAGE, EXT_LAYOUTS = 0x1, 0x2, 0x4
 HOT_FP16, HOT_BF16 = 0, 1
@@ -23,10 +23,11 @@ HOT_FP16, HOT_BF16 = 0, 1
 # Every symbol include/ztcp.h declares.
 EXPORTS = (
     "ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes",
-    "ztcp_egress_peak_into", "ztcp_egress_batch",
+    "ztcp_egress_peak_into", "ztcp_egress_peak_into_ext", "ztcp_egress_batch",
     "ztcp_ingress_peak_into", "ztcp_ingress_batch",
     "ztcp_chacha20_xor", "ztcp_siphash128",
-    "ztcp_selftest", "ztcp_device_diag", "ztcp_strerror",
+    "ztcp_selftest", "ztcp_device_diag", "ztcp_debug_spin_limit", "ztcp_strerror",
+    "ztcp_last_error",
 )
 
 # Every symbol include/ztcp_keyring.h declares (host code, callable without a GPU).
@@ -88,7 +89,9 @@ def lib() -> C.CDLL:
         f.restype = C.c_size_t
     L.ztcp_egress_peak_into.argtypes = [P, P, P, P, i64, G, i64, i64, i64, A, u64, K, P]
     L.ztcp_egress_peak_into.restype = i32
-    L.ztcp_egress_batch.argtypes = [P, i64, G, i64, i64, i64, u32, u32, K, P]
+    L.ztcp_egress_peak_into_ext.argtypes = [P, P, P, P, i64, G, i64, i64, i64, A, u64, K, u32, P]
+    L.ztcp_egress_peak_into_ext.restype = i32
+    L.ztcp_egress_batch.argtypes = [P, i64, G, i64, i64, i64, u32, u32, K, u32, P]
     L.ztcp_egress_batch.restype = i32
     L.ztcp_ingress_peak_into.argtypes = [P, i64, P, P, P, i64, G, u32, u32, u16, K, P, u32, P]
     L.ztcp_ingress_peak_into.restype = i32
@@ -102,8 +105,12 @@ def lib() -> C.CDLL:
     L.ztcp_selftest.restype = i32
     L.ztcp_device_diag.argtypes = []
     L.ztcp_device_diag.restype = i32
+    L.ztcp_debug_spin_limit.argtypes = [i64]
+    L.ztcp_debug_spin_limit.restype = i64
     L.ztcp_strerror.argtypes = [i32]
     L.ztcp_strerror.restype = C.c_char_p
+    L.ztcp_last_error.argtypes = []
+    L.ztcp_last_error.restype = C.c_char_p
     _bind_keyring(L)
     _lib = L
     return L
@@ -143,6 +150,11 @@ def _bind_keyring(L: C.CDLL) -> None:
 
 def strerror(code: int) -> str:
     return lib().ztcp_strerror(code).decode()
+
+
+def last_error() -> str:
+    """Why this thread's last call returned EINVAL / EOVERLAP (the reference's message)."""
+    return lib().ztcp_last_error().decode()
 
 
 def geometry(num_tokens: int, num_heads: int, head_dim: int, rope_dim: int, hot_dtype: int,

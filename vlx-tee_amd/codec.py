@@ -69,10 +69,11 @@ class NativeHipFusedColdPageCodec:
 
     def __init__(self, geometry: ColdPageGeometry, keyring: EphemeralSessionKeyRing,
                  dtype: torch.dtype = torch.float16, accept_extension_layouts: bool = False) -> None:
-        """``accept_extension_layouts``: decode pages whose headers carry this
-        codec's extension presets / RoPE mode (QuantPreset 4..6,
-        RoPEMode.PRESERVE_E4M3); by default they fail the flags check as in the
-        reference (KVIntegrityError)."""
+        """``accept_extension_layouts``: encode with, and decode pages whose
+        headers carry, this codec's extension presets / RoPE mode (QuantPreset
+        4..6, RoPEMode.PRESERVE_E4M3); by default egress rejects them as
+        invalid arguments and ingress fails them at the flags check, as the
+        reference does (cpp:1947-1948; KVIntegrityError)."""
         if dtype not in (torch.float16, torch.bfloat16):
             raise ValueError("dtype must be torch.float16 or torch.bfloat16")
         self.geometry = geometry
@@ -287,7 +288,7 @@ class NativeHipFusedColdPageCodec:
             int(aad_template.rope_mode), self.geometry.rope_dim, expected_payload,
             aad_template.tenant_id_hash, aad_template.model_id_hash, aad_template.layer_id,
             aad_template.head_group_id, aad_template.sequence_nonce & 0xFFFFFFFFFFFFFFFF,
-            **_keys(enc_key, mac_key))
+            **_keys(enc_key, mac_key), ext_layouts=self.accept_extension_layouts)
 
     def encode_cold_pages_batch_tensor(self, k_pages_cpu: torch.Tensor, v_pages_cpu: torch.Tensor | None,
                                        page_token_hashes_i64: torch.Tensor, tenant_id: str, session_id: str,

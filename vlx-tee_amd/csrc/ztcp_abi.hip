@@ -6,6 +6,7 @@
 // (ztcp_egress.hip / ztcp_ingress.hip) when the page layout is cut into whole
 // 64-byte keystream blocks and every pointer is 16-byte aligned, otherwise
 // the generic kernels (ztcp_generic.hip).
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -15,59 +16,110 @@ using namespace ztcp;
 
 namespace {
 
+// Per-call ingress state: a pool of CallState slots per device.  A call takes
+// a free slot for its duration; a synchronous call returns it after reading
+// the verdict, an asynchronous one records an event after its last kernel and
+// the slot is free again once that event has completed.
+constexpr int kCallSlots = 64;
 
 struct DeviceCtx {
-    DeviceState* state = nullptr;
-    unsigned long long* host_fail = nullptr;  // pinned
-    int32_t* status_scratch = nullptr;
-    int64_t status_cap = 0;
+    DeviceState* state = nullptr;      // sticky diagnostics (ztcp_device_diag)
+    CallState* calls = nullptr;        // [kCallSlots], device
+    CallState* host_calls = nullptr;   // [kCallSlots], pinned: verdict read-back
+    hipEvent_t done[kCallSlots] = {};
+    bool busy[kCallSlots] = {};
+    int next = 0;
     int cu_count = 0;
 };
 
-std::mutex g_mu;
-std::vector<DeviceCtx> g_ctx;
+std::mutex g_mu;                       // guards g_ctx and every DeviceCtx's slot bookkeeping
+std::vector<DeviceCtx*> g_ctx;
+std::atomic<uint32_t> g_spin_limit{kSpinLimit};
+thread_local const char* t_last_error = "";
+
+int fail_arg(int rc, const char* why) {
+    t_last_error = why;
+    return rc;
+}
 
 // Per-device library state, created on the first call on that device.
 int device_ctx(DeviceCtx** out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return ZTCP_EHIP;
     std::lock_guard<std::mutex> lock(g_mu);
-    if ((int)g_ctx.size() <= dev) g_ctx.resize(dev + 1);
-    DeviceCtx& c = g_ctx[dev];
-    if (!c.state) {
-        DeviceState* st = nullptr;
-        if (hipMalloc(&st, sizeof(DeviceState)) != hipSuccess) return ZTCP_EHIP;
-        DeviceState init{};
-        init.fail = ~0ull;
-        if (hipMemcpy(st, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess) return ZTCP_EHIP;
-        if (hipHostMalloc(&c.host_fail, sizeof(unsigned long long), hipHostMallocDefault) != hipSuccess)
-            return ZTCP_EHIP;
-        if (hipDeviceGetAttribute(&c.cu_count, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            return ZTCP_EHIP;
-        c.state = st;
+    if ((int)g_ctx.size() <= dev) g_ctx.resize(dev + 1, nullptr);
+    if (!g_ctx[dev]) {
+        DeviceCtx* c = new DeviceCtx();
+        const DeviceState init{};
+        bool ok = hipMalloc(&c->state, sizeof(DeviceState)) == hipSuccess &&
+                  hipMemcpy(c->state, &init, sizeof init, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMalloc(&c->calls, sizeof(CallState) * kCallSlots) == hipSuccess &&
+                  hipHostMalloc(&c->host_calls, sizeof(CallState) * kCallSlots, hipHostMallocDefault) == hipSuccess &&
+                  hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+        for (int i = 0; ok && i < kCallSlots; ++i)
+            ok = hipEventCreateWithFlags(&c->done[i], hipEventDisableTiming) == hipSuccess;
+        if (!ok) return ZTCP_EHIP;  // the partial context is left unused (one per device, process lifetime)
+        g_ctx[dev] = c;
     }
-    *out = &c;
+    *out = g_ctx[dev];
     return ZTCP_OK;
 }
 
-int status_scratch(DeviceCtx* c, int64_t n, int32_t** out) {
+// A free call slot: one never used, released, or whose asynchronous call's
+// event has completed.  When all are in flight, waits for the oldest.
+int acquire_call(DeviceCtx* c, int* slot) {
+    std::unique_lock<std::mutex> lock(g_mu);
+    for (;;) {
+        for (int i = 0; i < kCallSlots; ++i) {
+            const int k = (c->next + i) % kCallSlots;
+            if (c->busy[k]) {
+                const hipError_t q = hipEventQuery(c->done[k]);
+                if (q == hipErrorNotReady) continue;
+                if (q != hipSuccess) return ZTCP_EHIP;
+            }
+            c->busy[k] = true;
+            c->next = (k + 1) % kCallSlots;
+            *slot = k;
+            return ZTCP_OK;
+        }
+        const hipEvent_t oldest = c->done[c->next];
+        lock.unlock();
+        if (hipEventSynchronize(oldest) != hipSuccess) return ZTCP_EHIP;
+        lock.lock();
+    }
+}
+
+// Asynchronous release: the slot is free once the work enqueued on `stream`
+// so far has completed.  Synchronous release: free now.
+int release_call(DeviceCtx* c, int slot, hipStream_t stream, bool async) {
     std::lock_guard<std::mutex> lock(g_mu);
-    if (c->status_cap < n) {
-        if (c->status_scratch) (void)hipFree(c->status_scratch);
-        c->status_scratch = nullptr;
-        c->status_cap = 0;
-        if (hipMalloc(&c->status_scratch, (size_t)n * sizeof(int32_t)) != hipSuccess) return ZTCP_EHIP;
-        c->status_cap = n;
+    if (async) {
+        if (hipEventRecord(c->done[slot], stream) == hipSuccess) return ZTCP_OK;
+        // the event did not record: keep the slot out of use rather than
+        // hand it to another call while this one may still write it
+        return ZTCP_EHIP;
     }
-    *out = c->status_scratch;
+    c->busy[slot] = false;
     return ZTCP_OK;
 }
 
-bool geometry_ok(const ztcp_geometry* g) {  // cpp:1925-1935
-    return g && g->num_tokens > 0 && g->num_heads > 0 && g->head_dim >= 16 && g->head_dim % 16 == 0 &&
-           g->rope_dim >= 0 && g->rope_dim <= g->head_dim && g->rope_dim % 16 == 0 &&
-           (g->hot_dtype == ZTCP_HOT_FP16 || g->hot_dtype == ZTCP_HOT_BF16) &&
-           g->num_tokens * g->num_heads * g->head_dim < (int64_t)1 << 30;
+WaitSink wait_sink(DeviceCtx* c, CallState* call) {
+    return WaitSink{&c->state->diag, call ? &call->diag : nullptr, g_spin_limit.load(std::memory_order_relaxed)};
+}
+
+// The reference's dimension checks (cpp:1934-1935 egress, cpp:2277-2278
+// ingress) with its messages; `what` names the page tensor.
+int check_geometry(const ztcp_geometry* g, int64_t batch, const char* dims_msg) {
+    if (!g) return fail_arg(ZTCP_EINVAL, "geometry must not be NULL");
+    if (!(batch > 0 && g->num_tokens > 0 && g->num_heads > 0 && g->head_dim >= 16 && g->head_dim % 16 == 0))
+        return fail_arg(ZTCP_EINVAL, dims_msg);
+    if (!(g->rope_dim >= 0 && g->rope_dim <= g->head_dim && g->rope_dim % 16 == 0))
+        return fail_arg(ZTCP_EINVAL, "Invalid rope_dim");
+    if (g->hot_dtype != ZTCP_HOT_FP16 && g->hot_dtype != ZTCP_HOT_BF16)
+        return fail_arg(ZTCP_EINVAL, "hot_dtype must be ZTCP_HOT_FP16 or ZTCP_HOT_BF16");
+    if (g->num_tokens * g->num_heads * g->head_dim >= (int64_t)1 << 30)
+        return fail_arg(ZTCP_EINVAL, "page too large (num_tokens * num_heads * head_dim must be below 2^30)");
+    return ZTCP_OK;
 }
 
 bool overlap(const void* a, int64_t an, const void* b, int64_t bn) {  // cpp:1428-1437
@@ -99,26 +151,39 @@ int pages_per_group(int64_t batch, int cu_count) {
 int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blobs,
                   const ztcp_page_desc* descs, int64_t batch, const ztcp_geometry* g,
                   int64_t preset, int64_t rope_mode, int64_t expected_payload, const ztcp_aad* aad,
-                  uint64_t base_seq, const ztcp_keys* keys, hipStream_t stream) {
-    if (!geometry_ok(g) || batch <= 0 || !aad || !keys) return ZTCP_EINVAL;
-    if (!flags_valid(preset, rope_mode)) return ZTCP_EINVAL;
+                  uint64_t base_seq, const ztcp_keys* keys, uint32_t flags, hipStream_t stream) {
+    t_last_error = "";
+    int rc = check_geometry(g, batch, "Invalid k_pages dimensions");
+    if (rc) return rc;
+    if (!aad || !keys) return fail_arg(ZTCP_EINVAL, "aad and keys must not be NULL");
+    // cpp:1947-1948; the extension presets only when the call asks for them
+    const bool ext = (flags & ZTCP_EXT_LAYOUTS) != 0;
+    if (preset < 1 || preset > (ext ? 6 : 3))
+        return fail_arg(ZTCP_EINVAL, ext ? "Invalid preset (must be 1..6)" : "Invalid preset (must be 1..3)");
+    if (rope_mode < 0 || rope_mode > (ext ? 3 : 2))
+        return fail_arg(ZTCP_EINVAL, ext ? "Invalid rope_mode (must be 0..3)" : "Invalid rope_mode (must be 0..2)");
     const int64_t vecs = g->num_tokens * g->num_heads;
     const bool has_v = descs ? !g->is_mla_single_buffer : (v != nullptr);
     Layout lay;
-    if (!build_layout(preset, rope_mode, vecs, g->head_dim, g->rope_dim, has_v, lay)) return ZTCP_EINVAL;
-    if (expected_payload < (int64_t)lay.required || expected_payload > ((int64_t)1 << 31))
-        return ZTCP_EINVAL;  // cpp:1955-1957
+    if (!build_layout(preset, rope_mode, vecs, g->head_dim, g->rope_dim, has_v, lay))
+        return fail_arg(ZTCP_EINVAL, "head_dim / rope_dim not divisible by the extension preset's group size");
+    if (expected_payload < (int64_t)lay.required)
+        return fail_arg(ZTCP_EINVAL, "expected_payload_bytes smaller than required payload");  // cpp:1955-1957
+    if (expected_payload > ((int64_t)1 << 31))
+        return fail_arg(ZTCP_EINVAL, "expected_payload_bytes too large (at most 2^31)");
     const int64_t blob_bytes = kHeader + expected_payload + kTag;
     const int64_t page_bytes = vecs * g->head_dim * 2;
     if (!descs) {
-        if (!k || !tok || !blobs) return ZTCP_EINVAL;
-        const int64_t out_n = blob_bytes * batch;  // cpp:1949-1951
-        if (overlap(blobs, out_n, k, page_bytes * batch) || overlap(blobs, out_n, v, page_bytes * batch) ||
-            overlap(blobs, out_n, tok, 8 * batch))
-            return ZTCP_EOVERLAP;
+        if (!k || !blobs) return fail_arg(ZTCP_EINVAL, "k_pages and out_blobs must not be NULL");
+        if (!tok) return fail_arg(ZTCP_EINVAL, "page_token_hashes must not be NULL");
+        const int64_t out_n = blob_bytes * batch;  // cpp:1940, cpp:1949-1951
+        if (overlap(blobs, out_n, k, page_bytes * batch) || overlap(blobs, out_n, tok, 8 * batch))
+            return fail_arg(ZTCP_EOVERLAP, "out_blobs must not alias or overlap input tensors");
+        if (overlap(blobs, out_n, v, page_bytes * batch))
+            return fail_arg(ZTCP_EOVERLAP, "out_blobs must not alias or overlap v_pages");
     }
     DeviceCtx* ctx = nullptr;
-    int rc = device_ctx(&ctx);
+    rc = device_ctx(&ctx);
     if (rc) return rc;
 
     EgressParams p{};
@@ -137,15 +202,15 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
     p.key = key_words(keys);
     p.mk0 = keys->mk0;
     p.mk1 = keys->mk1;
-    const uint64_t flags = (uint64_t)((preset & 0x0F) | ((rope_mode & 0x0F) << 4));
-    p.hdr0 = (uint64_t)kMagic | ((uint64_t)kVersion << 16) | (flags << 24) |
+    const uint64_t hflags = (uint64_t)((preset & 0x0F) | ((rope_mode & 0x0F) << 4));
+    p.hdr0 = (uint64_t)kMagic | ((uint64_t)kVersion << 16) | (hflags << 24) |
              ((uint64_t)aad->tenant_id_hash << 32);
     p.hdr1 = (uint64_t)aad->model_id_hash | ((uint64_t)aad->layer_id << 32) |
              ((uint64_t)aad->head_group_id << 48);
     p.nonce2 = ((uint32_t)aad->layer_id << 16) | (uint32_t)aad->head_group_id;  // cpp:108-109
     p.base_seq = base_seq;
     p.ppw = pages_per_group(batch, ctx->cu_count);
-    p.state = ctx->state;
+    p.sink = wait_sink(ctx, nullptr);
 
     const bool fast = lay.aligned && expected_payload == (int64_t)lay.required && blob_bytes % 16 == 0 &&
                       (descs || (aligned16(k) && aligned16(v) && aligned16(blobs)));
@@ -158,23 +223,31 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
                    void* out_v, const ztcp_page_desc* descs, int64_t batch, const ztcp_geometry* g,
                    uint32_t tenant, uint32_t model, uint16_t layer, const ztcp_keys* keys,
                    int32_t* page_status, uint32_t flags, hipStream_t stream) {
-    if (!geometry_ok(g) || batch <= 0 || !keys) return ZTCP_EINVAL;
-    if (blob_bytes <= (int64_t)(kHeader + kTag) || blob_bytes > ((int64_t)1 << 31)) return ZTCP_EINVAL;
-    if ((flags & ZTCP_ASYNC) && !page_status) return ZTCP_EINVAL;
+    t_last_error = "";
+    int rc = check_geometry(g, batch, "Invalid out_k_pages dimensions");
+    if (rc) return rc;
+    if (!keys) return fail_arg(ZTCP_EINVAL, "keys must not be NULL");
+    if (blob_bytes <= (int64_t)(kHeader + kTag)) return fail_arg(ZTCP_EINVAL, "cold_blob too small");  // cpp:2282
+    if (blob_bytes > ((int64_t)1 << 31)) return fail_arg(ZTCP_EINVAL, "cold_blob too large (at most 2^31 bytes)");
+    if ((flags & ZTCP_ASYNC) && !page_status)
+        return fail_arg(ZTCP_EINVAL, "ZTCP_ASYNC needs page_status (the verdicts' only destination)");
     const bool mla = g->is_mla_single_buffer != 0;
     const int64_t vecs = g->num_tokens * g->num_heads;
     const int64_t page_bytes = vecs * g->head_dim * 2;
     if (!descs) {
-        if (!blobs || !tok || !out_k) return ZTCP_EINVAL;
-        if (!mla && !out_v) return ZTCP_EINVAL;  // cpp:2288
+        if (!blobs || !out_k) return fail_arg(ZTCP_EINVAL, "cold_blobs and out_k_pages must not be NULL");
+        if (!tok) return fail_arg(ZTCP_EINVAL, "expected_token_hashes must not be NULL");
+        if (!mla && !out_v) return fail_arg(ZTCP_EINVAL, "out_v_pages is required for non-MLA geometry");  // cpp:2288
         const int64_t kn = page_bytes * batch, bn = blob_bytes * batch;
-        if (overlap(out_k, kn, blobs, bn) || overlap(out_k, kn, tok, 8 * batch) ||
-            (!mla && (overlap(out_v, kn, blobs, bn) || overlap(out_v, kn, tok, 8 * batch) ||
-                      overlap(out_k, kn, out_v, kn))))  // cpp:2283, cpp:2293-2294
-            return ZTCP_EOVERLAP;
+        if (overlap(out_k, kn, blobs, bn) || overlap(out_k, kn, tok, 8 * batch))  // cpp:2283
+            return fail_arg(ZTCP_EOVERLAP, "out_k_pages must not alias or overlap input tensors");
+        if (!mla && overlap(out_k, kn, out_v, kn))  // cpp:2292
+            return fail_arg(ZTCP_EOVERLAP, "out_k_pages and out_v_pages must not alias or overlap in memory");
+        if (!mla && (overlap(out_v, kn, blobs, bn) || overlap(out_v, kn, tok, 8 * batch)))  // cpp:2293-2294
+            return fail_arg(ZTCP_EOVERLAP, "out_v_pages must not alias or overlap input tensors");
     }
     DeviceCtx* ctx = nullptr;
-    int rc = device_ctx(&ctx);
+    rc = device_ctx(&ctx);
     if (rc) return rc;
 
     IngressParams p{};
@@ -212,34 +285,45 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
     p.exp_model = model;
     p.exp_layer = layer;
     p.per_page = (flags & ZTCP_PER_PAGE) ? 1 : 0;
-    p.state = ctx->state;
     p.ppw = pages_per_group(batch, ctx->cu_count);
-
+    const bool async = (flags & ZTCP_ASYNC) != 0;
     const bool fast = all_aligned && blob_bytes % 16 == 0 &&
                       (descs || (aligned16(blobs) && aligned16(out_k) && (mla || aligned16(out_v))));
-    hipError_t e = launch_reset_fail(p.state, stream);
-    if (e == hipSuccess) {
-        if (fast) {
-            e = launch_ingress_fused(p, g->hot_dtype, stream);
-            if (e == hipSuccess && !p.per_page) e = launch_ingress_finalize(p, stream);
-        } else {
-            p.n_units = (int32_t)(vecs * (g->head_dim / 16) * (mla ? 1 : 2));  // groups per page
-            int32_t* status = page_status;
-            if (!status) {
-                rc = status_scratch(ctx, batch, &status);
-                if (rc) return rc;
-            }
-            e = launch_ingress_generic_impl(p, g->hot_dtype, status, stream);
-        }
+    p.n_units = (int32_t)(vecs * (g->head_dim / 16) * (mla ? 1 : 2));  // generic path: groups per page
+
+    int slot = 0;
+    rc = acquire_call(ctx, &slot);
+    if (rc) return rc;
+    p.call = ctx->calls + slot;
+    p.sink = wait_sink(ctx, p.call);
+    // The generic path needs every page's status between its kernels; without
+    // the caller's array it takes a stream-ordered allocation of its own.
+    int32_t* status = page_status;
+    bool own_status = false;
+    hipError_t e = launch_reset_call(p.call, stream);
+    if (e == hipSuccess && !fast && !status) {
+        e = hipMallocAsync((void**)&status, (size_t)batch * sizeof(int32_t), stream);
+        own_status = e == hipSuccess;
     }
+    if (e == hipSuccess) {
+        e = fast ? launch_ingress_fused(p, g->hot_dtype, stream)
+                 : launch_ingress_generic_impl(p, g->hot_dtype, status, stream);
+        if (e == hipSuccess && fast && !p.per_page) e = launch_ingress_finalize(p, stream);
+    }
+    if (own_status && hipFreeAsync(status, stream) != hipSuccess && e == hipSuccess) e = hipErrorUnknown;
+    if (e == hipSuccess && !async)
+        e = hipMemcpyAsync(ctx->host_calls + slot, p.call, sizeof(CallState), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess && !async) e = hipStreamSynchronize(stream);
+    // read the verdict while the slot (and its read-back area) is still ours
+    const CallState r = (e == hipSuccess && !async) ? ctx->host_calls[slot] : CallState{~0ull, 0u, 0u};
+    // a failed launch leaves the slot to an event, as the kernels before it
+    // may still run
+    const int rel = release_call(ctx, slot, stream, async || e != hipSuccess);
     if (e != hipSuccess) return ZTCP_EHIP;
-    if (flags & ZTCP_ASYNC) return ZTCP_OK;
-    if (hipMemcpyAsync(ctx->host_fail, &p.state->fail, sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                       stream) != hipSuccess ||
-        hipStreamSynchronize(stream) != hipSuccess)
-        return ZTCP_EHIP;
-    const unsigned long long f = *ctx->host_fail;
-    return f == ~0ull ? ZTCP_OK : (int)(f & 0xFFu);
+    if (rel) return rel;
+    if (async) return ZTCP_OK;
+    if (r.diag) return ZTCP_EDEVICE;
+    return r.fail == ~0ull ? ZTCP_OK : (int)(r.fail & 0xFFu);
 }
 
 }  // namespace
@@ -265,24 +349,34 @@ size_t ztcp_blob_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode
     return r == (size_t)-1 ? r : r + kHeader + kTag;
 }
 
+int ztcp_egress_peak_into_ext(const void* k_pages, const void* v_pages, const int64_t* page_token_hashes,
+                              uint8_t* out_blobs, int64_t batch, const ztcp_geometry* g, int64_t preset,
+                              int64_t rope_mode, int64_t expected_payload_bytes, const ztcp_aad* aad,
+                              uint64_t base_sequence_nonce, const ztcp_keys* keys, uint32_t flags,
+                              void* stream) {
+    if (g && g->is_mla_single_buffer && v_pages)
+        return fail_arg(ZTCP_EINVAL, "v_pages must be NULL for an MLA single-buffer geometry");
+    return egress_common(k_pages, v_pages, page_token_hashes, out_blobs, nullptr, batch, g, preset,
+                         rope_mode, expected_payload_bytes, aad, base_sequence_nonce, keys, flags,
+                         (hipStream_t)stream);
+}
+
 int ztcp_egress_peak_into(const void* k_pages, const void* v_pages, const int64_t* page_token_hashes,
                           uint8_t* out_blobs, int64_t batch, const ztcp_geometry* g, int64_t preset,
                           int64_t rope_mode, int64_t expected_payload_bytes, const ztcp_aad* aad,
                           uint64_t base_sequence_nonce, const ztcp_keys* keys, void* stream) {
-    if (g && g->is_mla_single_buffer && v_pages) return ZTCP_EINVAL;
-    return egress_common(k_pages, v_pages, page_token_hashes, out_blobs, nullptr, batch, g, preset,
-                         rope_mode, expected_payload_bytes, aad, base_sequence_nonce, keys,
-                         (hipStream_t)stream);
+    return ztcp_egress_peak_into_ext(k_pages, v_pages, page_token_hashes, out_blobs, batch, g, preset, rope_mode,
+                                     expected_payload_bytes, aad, base_sequence_nonce, keys, 0u, stream);
 }
 
 int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages, const ztcp_geometry* g,
                       int64_t preset, int64_t rope_mode, int64_t expected_payload_bytes,
                       uint32_t tenant_id_hash, uint32_t model_id_hash, const ztcp_keys* keys,
-                      void* stream) {
-    if (!pages) return ZTCP_EINVAL;
+                      uint32_t flags, void* stream) {
+    if (!pages) return fail_arg(ZTCP_EINVAL, "pages must not be NULL");
     const ztcp_aad aad{tenant_id_hash, model_id_hash, 0, 0};  // layer / head group per page
     return egress_common(nullptr, nullptr, nullptr, nullptr, pages, n_pages, g, preset, rope_mode,
-                         expected_payload_bytes, &aad, 0, keys, (hipStream_t)stream);
+                         expected_payload_bytes, &aad, 0, keys, flags, (hipStream_t)stream);
 }
 
 int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
@@ -298,7 +392,7 @@ int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
 int ztcp_ingress_batch(const ztcp_page_desc* pages, int64_t n_pages, int64_t blob_bytes,
                        const ztcp_geometry* g, uint32_t expected_tenant_hash, uint32_t expected_model_hash,
                        const ztcp_keys* keys, int32_t* page_status, uint32_t flags, void* stream) {
-    if (!pages) return ZTCP_EINVAL;
+    if (!pages) return fail_arg(ZTCP_EINVAL, "pages must not be NULL");
     return ingress_common(nullptr, blob_bytes, nullptr, nullptr, nullptr, pages, n_pages, g,
                           expected_tenant_hash, expected_model_hash, 0, keys, page_status, flags,
                           (hipStream_t)stream);
@@ -355,18 +449,26 @@ int ztcp_device_diag(void) {
     return (int)d;
 }
 
+int64_t ztcp_debug_spin_limit(int64_t n) {
+    const uint32_t v = n < 0 ? kSpinLimit : (n > (int64_t)0xFFFFFFFFu ? 0xFFFFFFFFu : (uint32_t)n);
+    return (int64_t)g_spin_limit.exchange(v);
+}
+
 const char* ztcp_strerror(int code) {
     switch (code) {
         case ZTCP_OK: return "ok";
         case ZTCP_ERR_HEADER: return "KV_INTEGRITY_ERROR: Invalid cold-page header magic, version, or flags";
         case ZTCP_ERR_AAD: return "CROSS_TENANT_CONTAMINATION: Cold-page AAD mismatch";
         case ZTCP_ERR_MAC: return "KV_INTEGRITY_ERROR: Cold-page MAC verification failed";
+        case ZTCP_ERR_DEVICE: return "KV_INTEGRITY_ERROR: page rejected after a device-side wait expired";
         case ZTCP_EINVAL: return "invalid argument";
         case ZTCP_EOVERLAP: return "outputs must not alias or overlap input tensors";
         case ZTCP_EHIP: return "HIP runtime error";
-        case ZTCP_EDEVICE: return "device-side bounded wait expired";
+        case ZTCP_EDEVICE: return "device-side bounded wait expired; outputs zeroed";
         default: return "unknown error";
     }
 }
+
+const char* ztcp_last_error(void) { return t_last_error; }
 
 }  // extern "C"

@@ -69,7 +69,8 @@ constexpr int kFlagScale = kFlagCount + kStage;       // [kScaleSlots] unit + 1:
 constexpr int kFlagMacUsed = kFlagScale + kScaleSlots;  // rows absorbed by the MAC wave
 constexpr int kFlagStored = kFlagMacUsed + 1;         // rows passed by the storer wave
 constexpr int kFlagTask = kFlagStored + 1;            // next code row to hand out
-constexpr int kNumFlags = (kFlagTask + 2) & ~1;  // even: the blob table after it is 8-byte aligned
+constexpr int kFlagExpired = kFlagTask + 1;           // 1: a bounded wait of the workgroup expired
+constexpr int kNumFlags = (kFlagExpired + 2) & ~1;    // even: the blob table after it is 8-byte aligned
 constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byte aligned)
 constexpr int kLdsWords = kLdsBlobs + 2 * 64;
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
@@ -165,6 +166,7 @@ struct ProducerCtx {
     // compiler wait for all outstanding stores before the next row's loads).
     uint8_t* sb[4];   // blob of the page stored by store k
     uint32_t sq[4];   // byte offset of that page's quad inside a row slot
+    Waiter wt;
 
     __device__ __forceinline__ void init_stores(int ppw) {
         const uint64_t* blobs = reinterpret_cast<const uint64_t*>(lds + kLdsBlobs);
@@ -309,7 +311,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     if (kind != kSecRaw) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
         uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
-        wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, p.state);
+        wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, c.wt);
         const int sw = param_words_per_row(kind);  // parameter words of this row: 2, 4 or 1
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -322,8 +324,8 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     uint32_t ks[16];
     st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
     uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
-    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, p.state);
-    wait_ge<kDiagEgressWait>(&flags[kFlagStored], row.mrow - kRing + 1, p.state);
+    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, c.wt);
+    wait_ge<kDiagEgressWait>(&flags[kFlagStored], row.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad(slot, c.lane, q,
@@ -343,6 +345,7 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     c.n2 = c.pg.nonce2;
     c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
+    c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     c.init_stores(ppw);
     const int32_t total = total_code_rows(p.lay);
     // The page descriptor and kernel argument loads above complete here,
@@ -450,9 +453,9 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     m.init(p.lay);
     // Rows arrive in MAC order in the ring (code rows from the producers,
     // scale rows from the feeder), so the next row is always the next slot.
-    DeviceState* st = p.state;
+    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     __builtin_amdgcn_s_waitcnt(0);
-    mac_rows<kRing, kDiagEgressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
+    mac_rows<kRing, kDiagEgressWait>(wt, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
                                      m.total, [](int32_t, int, const uint4&) {});
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
@@ -470,9 +473,9 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
 // current one is written; a section's first row is never waited for before
 // the previous section's rows are all in the ring, so the MAC wave never
 // depends on a row that needs it to progress first.
-__device__ __forceinline__ void feed_load(const EgressParams& p, const uint32_t* lds, const uint8_t* src,
+__device__ __forceinline__ void feed_load(const Waiter& wt, const uint32_t* lds, const uint8_t* src,
                                           int32_t g, uint4 (&x)[4]) {
-    wait_ge<kDiagEgressWait>(lds + kLdsFlags + kFlagScale + g % kScaleSlots, g + 1, p.state);
+    wait_ge<kDiagEgressWait>(lds + kLdsFlags + kFlagScale + g % kScaleSlots, g + 1, wt);
     if (src) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) x[q] = ldg16(src, q);
@@ -482,11 +485,11 @@ __device__ __forceinline__ void feed_load(const EgressParams& p, const uint32_t*
     }
 }
 
-__device__ __forceinline__ void feed_put(const EgressParams& p, uint32_t* lds, const PageQuads& pq, int32_t rs,
+__device__ __forceinline__ void feed_put(const Waiter& wt, uint32_t* lds, const PageQuads& pq, int32_t rs,
                                          const uint4 (&x)[4]) {
     uint32_t* flags = lds + kLdsFlags;
-    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], rs - kRing + 1, p.state);
-    wait_ge<kDiagEgressWait>(&flags[kFlagStored], rs - kRing + 1, p.state);
+    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], rs - kRing + 1, wt);
+    wait_ge<kDiagEgressWait>(&flags[kFlagStored], rs - kRing + 1, wt);
     uint32_t* slot = lds + (rs % kRing) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
@@ -500,6 +503,7 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
     pq.init(lane);
     MacPlan m;
     m.init(p.lay);
+    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     int32_t g0 = 0, r0 = 0;  // scale rows / MAC rows before the section
 #pragma unroll
     for (int si = 0; si < 3; ++si) {
@@ -508,14 +512,14 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
         const uint32_t so = si == 0 ? m.so0 : (si == 1 ? m.so1 : m.so2);
         const uint8_t* base = blob ? blob + kHeader + so : nullptr;
         uint4 a[4], b[4];
-        if (n > 0) feed_load(p, lds, base, g0, a);
+        if (n > 0) feed_load(wt, lds, base, g0, a);
 #pragma unroll 1
         for (int32_t j = 0; j < n; j += 2) {
-            if (j + 1 < n) feed_load(p, lds, base ? base + 64u * (uint32_t)(j + 1) : nullptr, g0 + j + 1, b);
-            feed_put(p, lds, pq, rs + j, a);
+            if (j + 1 < n) feed_load(wt, lds, base ? base + 64u * (uint32_t)(j + 1) : nullptr, g0 + j + 1, b);
+            feed_put(wt, lds, pq, rs + j, a);
             if (j + 1 >= n) break;
-            if (j + 2 < n) feed_load(p, lds, base ? base + 64u * (uint32_t)(j + 2) : nullptr, g0 + j + 2, a);
-            feed_put(p, lds, pq, rs + j + 1, b);
+            if (j + 2 < n) feed_load(wt, lds, base ? base + 64u * (uint32_t)(j + 2) : nullptr, g0 + j + 2, a);
+            feed_put(wt, lds, pq, rs + j + 1, b);
         }
         g0 += n;
         r0 = rs + n;
@@ -540,6 +544,7 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
     c.p = &p;
     c.lane = threadIdx.x & 63;
     c.lds = lds;
+    c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     c.init_stores(ppw);
     MacPlan m;
     m.init(p.lay);
@@ -550,7 +555,7 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
     for (int32_t r = 0; r < m.total; ++r) {
         const bool scale = (r >= s0 && r < s0 + m.ns0) || (r >= s1 && r < s1 + m.ns1) || (r >= s2 && r < s2 + m.ns2);
         if (!scale) {
-            wait_ge<kDiagEgressWait>(&flags[kFlagRing + r % kRing], r + 1, p.state);
+            wait_ge<kDiagEgressWait>(&flags[kFlagRing + r % kRing], r + 1, c.wt);
             store_row(lds + (r % kRing) * kRowWords, c, (uint32_t)kHeader + 64u * (uint32_t)r);
         }
         publish(&flags[kFlagStored], (uint32_t)r + 1u);  // the release orders the slot reads before it
@@ -573,18 +578,26 @@ __global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressPara
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
         egress_mac<DT>(p, page0, ppw, lds);
-        return;
-    }
-    if (wave == 4) {
+    } else if (wave == 4) {
         egress_scale_feed(p, lds);
-        return;
-    }
-    if ((wave & 3) == 0) return;  // the rest of the MAC wave's SIMD stays idle
-    if (wave == 1) {
+    } else if ((wave & 3) == 0) {
+        // the rest of the MAC wave's SIMD stays idle
+    } else if (wave == 1) {
         egress_store_rows(p, page0, ppw, lds);
-        return;
+    } else {
+        egress_produce<DT, FAM>(p, page0, ppw, lds);
     }
-    egress_produce<DT, FAM>(p, page0, ppw, lds);
+    // Fail closed: if any bounded wait of the workgroup expired, its rows may
+    // have been read or overwritten out of turn, so no blob of the workgroup
+    // may verify.  The MAC wave's lanes, which stored the headers, zero the
+    // first 16 header bytes (magic 0: every ingress rejects the page with
+    // status 1).  Same lanes, same addresses: the stores stay in order.
+    __syncthreads();
+    if (__hip_atomic_load(lds + kLdsFlags + kFlagExpired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u &&
+        (int)threadIdx.x < ppw) {
+        uint8_t* blob = reinterpret_cast<uint8_t*>(reinterpret_cast<const uint64_t*>(lds + kLdsBlobs)[threadIdx.x]);
+        stg16(blob, 0, make_uint4(0u, 0u, 0u, 0u));
+    }
 }
 
 }  // namespace

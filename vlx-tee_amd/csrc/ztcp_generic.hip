@@ -192,7 +192,7 @@ __global__ void ingress_generic_verify_kernel(IngressParams p, int32_t* status) 
             st = 1;
     }
     status[page] = st;
-    if (st != 0) atomicMin(&p.state->fail, ((unsigned long long)page << 8) | (unsigned long long)st);
+    if (st != 0) atomicMin(&p.call->fail, ((unsigned long long)page << 8) | (unsigned long long)st);
 }
 
 template <int DT>
@@ -258,7 +258,7 @@ __global__ void ingress_generic_decode_kernel(IngressParams p, int64_t groups_pe
 // Zero failing pages (per-page mode) or, when any page failed, every page
 // (all-or-nothing); byte stores keep any alignment legal.
 __global__ void ingress_generic_zero_kernel(IngressParams p, const int32_t* status, int all) {
-    if (all && p.state->fail == ~0ull) return;
+    if (all && p.call->fail == ~0ull) return;
     const int64_t total = p.page_bytes * p.batch;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {

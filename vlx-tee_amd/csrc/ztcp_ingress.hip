@@ -61,7 +61,8 @@ constexpr int kFlagMacUsed = kFlagCount + kStage;    // payload rows absorbed by
 constexpr int kFlagTask = kFlagMacUsed + 1;          // next row to hand out
 constexpr int kFlagStatus = kFlagTask + 1;           // [64] verdicts
 constexpr int kFlagNaN = kFlagStatus + 64;           // [64] 1: the page has an inf / NaN scale
-constexpr int kNumFlags = (kFlagNaN + 64 + 1) & ~1;  // even: the pointer table after it is 8-byte aligned
+constexpr int kFlagExpired = kFlagNaN + 64;          // 1: a bounded wait of the workgroup expired
+constexpr int kNumFlags = (kFlagExpired + 2) & ~1;   // even: the pointer table after it is 8-byte aligned
 constexpr int kLdsPtrs = kLdsFlags + kNumFlags;      // [2][64] output pointers (K, V)
 constexpr int kLdsLayouts = kLdsPtrs + 2 * 2 * 64;   // [kNumLayouts] Layout, one per header flags value
 constexpr int kLayoutWords = (int)(sizeof(Layout) / 4);
@@ -360,6 +361,7 @@ struct DecoderCtx {
     uint32_t* lds;
     uint32_t* tile;         // this wave's dequantized tile
     PageQuads pq;           // this lane's quads in a row slot
+    Waiter wt;
     int lane;
     // Transposed tile stores: store k (0..3) writes quad (lane & 3) of page
     // 16 k + (lane >> 2), whose output pointer is entry 16 k + (lane >> 2)
@@ -383,7 +385,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     uint32_t* flags = c.lds + kLdsFlags;
     // ciphertext to the verify wave, at its place in payload order
     uint32_t* slot = c.lds + (k.mrow % kRing) * kRowWords;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, p.state);
+    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
@@ -399,7 +401,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     uint32_t sc[SW];
     if constexpr (KIND != kSecRaw) {
         const int slot_s = k.g % kStage;
-        wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, p.state);
+        wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, c.wt);
         const uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
         if constexpr (KIND == kSecInt8) {  // words 2j, 2j + 1 of the page's scale row
             const uint32_t* w = stage + quad_word(c.lane, k.j >> 1) + 2 * (k.j & 1);
@@ -470,7 +472,7 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
     const IngressParams& p = *c.p;
     uint32_t* flags = c.lds + kLdsFlags;
     uint32_t* slot = c.lds + (k.mrow % kRing) * kRowWords;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, p.state);
+    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
@@ -485,7 +487,7 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
     if (nxt.valid) load_block(c.pay + 64u * (uint32_t)nxt.block, ct);
     uint32_t sc[2];
     const int slot_s = k.g % kStage;
-    wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, p.state);
+    wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, c.wt);
     const uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
     if constexpr (G::kParamWords == 2) {  // words 2j, 2j + 1 of the page's parameter row
         const uint32_t* w = stage + quad_word(c.lane, k.j >> 1) + 2 * (k.j & 1);
@@ -545,7 +547,7 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
     if (nxt.valid) load_block(c.pay + 64u * (uint32_t)nxt.block, ct);
     if (params_nonfinite(sc)) flags[kFlagNaN + c.lane] = 1u;
     const int slot_s = k.g % kStage;
-    wait_ge<kDiagIngressWait>(&flags[kFlagFree + slot_s], k.g - kStage + 1, p.state);
+    wait_ge<kDiagIngressWait>(&flags[kFlagFree + slot_s], k.g - kStage + 1, c.wt);
     uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -602,10 +604,10 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
 // from the blob into the ring, in payload order, two rows in flight.  It
 // depends only on the verify wave freeing slots, so the rows before any row
 // it waits for are always in the ring already.
-__device__ __forceinline__ void feed_put(const IngressParams& p, uint32_t* lds, const PageQuads& pq, int32_t r,
+__device__ __forceinline__ void feed_put(const Waiter& wt, uint32_t* lds, const PageQuads& pq, int32_t r,
                                          const uint4 (&x)[4]) {
     uint32_t* flags = lds + kLdsFlags;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], r - kRing + 1, p.state);
+    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], r - kRing + 1, wt);
     uint32_t* slot = lds + (r % kRing) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
@@ -616,6 +618,7 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
                              const uint8_t* pay, int lane) {
     PageQuads pq;
     pq.init(lane);
+    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     const int32_t total = (int32_t)(p.payload / 64u);
     // payload rows [cb_i, ce_i) are section i's code rows (decoders)
     int32_t cb[3], ce[3];
@@ -645,11 +648,11 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
     load(rb, b);
 #pragma unroll 1
     for (;;) {
-        feed_put(p, lds, pq, ra, a);
+        feed_put(wt, lds, pq, ra, a);
         if (rb >= total) break;
         ra = next_fed(rb + 1);
         load(ra, a);
-        feed_put(p, lds, pq, rb, b);
+        feed_put(wt, lds, pq, rb, b);
         if (ra >= total) break;
         rb = next_fed(ra + 1);
         load(rb, b);
@@ -678,7 +681,7 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     s.absorb_words<4>(hdr);
     PageQuads pq;
     pq.init(lane);
-    DeviceState* st = p.state;
+    const Waiter st = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     __builtin_amdgcn_s_waitcnt(0);
     mac_rows<kRing, kDiagIngressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
                                       total, [](int32_t, int, const uint4&) {});
@@ -747,6 +750,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         c.tile = lds + kLdsTile + (wave - 1 - (wave >> 2)) * kRowWords;
         c.lane = lane;
         c.pq.init(lane);
+        c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
         c.init_stores();
         decode_rows<DT, FAM>(c, lay);
     }
@@ -793,11 +797,18 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
+    // Fail closed: after an expired bounded wait, a page's verdict and its
+    // decoded bytes may come from rows handed over out of turn, so every page
+    // of the workgroup fails with ZTCP_ERR_DEVICE and its outputs are zeroed
+    // like any failing page's.
+    const bool expired = flags[kFlagExpired] != 0u;
+    if (expired && (int)threadIdx.x < ppw) flags[kFlagStatus + threadIdx.x] = (uint32_t)ZTCP_ERR_DEVICE;
+    __syncthreads();
     if ((int)threadIdx.x < ppw) {
         const int32_t st = (int32_t)flags[kFlagStatus + threadIdx.x];
         const int64_t pg = page0 + threadIdx.x;
         if (p.page_status) p.page_status[pg] = st;
-        if (st != 0) atomicMin(&p.state->fail, ((unsigned long long)pg << 8) | (unsigned long long)st);
+        if (st != 0) atomicMin(&p.call->fail, ((unsigned long long)pg << 8) | (unsigned long long)st);
     }
     if (p.per_page) {  // extension: zero only the failing pages
         const int64_t n16 = p.page_bytes / 16;
@@ -818,7 +829,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
 // All-or-nothing epilogue (cpp:2481-2486): if any page failed, zero both
 // outputs entirely.  Every block reads the failure word once.
 __global__ void ingress_finalize_kernel(IngressParams p) {
-    if (p.state->fail == ~0ull) return;
+    if (p.call->fail == ~0ull) return;
     const int64_t n16 = p.page_bytes / 16;
     const int64_t total = n16 * p.batch;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -830,7 +841,10 @@ __global__ void ingress_finalize_kernel(IngressParams p) {
     }
 }
 
-__global__ void reset_fail_kernel(DeviceState* st) { st->fail = ~0ull; }
+__global__ void reset_call_kernel(CallState* call) {
+    call->fail = ~0ull;
+    call->diag = 0u;
+}
 
 hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s) {
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
@@ -861,8 +875,8 @@ hipError_t launch_ingress_finalize(const IngressParams& p, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_reset_fail(DeviceState* st, hipStream_t s) {
-    hipLaunchKernelGGL(reset_fail_kernel, dim3(1), dim3(1), 0, s, st);
+hipError_t launch_reset_call(CallState* call, hipStream_t s) {
+    hipLaunchKernelGGL(reset_call_kernel, dim3(1), dim3(1), 0, s, call);
     return hipGetLastError();
 }
 

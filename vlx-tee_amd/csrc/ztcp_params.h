@@ -11,15 +11,34 @@
 
 namespace ztcp {
 
-// Sticky device diagnostics (bit flags, or-ed by kernels).
+// Diagnostic bits (or-ed by kernels).
 constexpr uint32_t kDiagEgressWait = 1u;   // a bounded wait of the fused egress kernel expired
 constexpr uint32_t kDiagIngressWait = 2u;  // a bounded wait of the fused ingress kernel expired
 
-// Per-device library state (allocated once per device by the host side).
+// Bounded waits give up after this many s_sleep(1) polls (about 30 ms).
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+// Per-device library state (allocated once per device by the host side):
+// sticky diagnostic bits, read and cleared by ztcp_device_diag.
 struct DeviceState {
-    uint32_t diag;             // sticky diagnostic flags
+    uint32_t diag;
+    uint32_t pad[3];
+};
+
+// Per-call ingress state: every ingress call owns one for its duration, so
+// concurrent calls on one device (other streams, other threads) never see
+// each other's verdicts.  Reset by the call's first kernel.
+struct CallState {
+    unsigned long long fail;   // (page_index << 8) | status of the lowest failing page; ~0 = none
+    uint32_t diag;             // kDiag* bits of waits that expired during this call
     uint32_t pad;
-    unsigned long long fail;   // (page_index << 8) | status of the lowest failing page
+};
+
+// What a bounded wait reports to when it expires.
+struct WaitSink {
+    uint32_t* dev_diag;        // DeviceState::diag (sticky, per device)
+    uint32_t* call_diag;       // CallState::diag, or nullptr (egress)
+    uint32_t spin_limit;       // polls before giving up
 };
 
 struct EgressParams {
@@ -42,7 +61,7 @@ struct EgressParams {
     uint32_t nonce2;               // (layer_id << 16) | head_group_id
     uint64_t base_seq;
     int32_t ppw;                   // pages per workgroup
-    DeviceState* state;
+    WaitSink sink;
 };
 
 struct IngressParams {
@@ -66,7 +85,8 @@ struct IngressParams {
     uint32_t exp_layer;
     int32_t per_page;              // zero failing pages in-kernel
     int32_t ppw;
-    DeviceState* state;
+    CallState* call;               // this call's failure word and diagnostics
+    WaitSink sink;
 };
 
 // Page addressing (contiguous batch or descriptor array).
@@ -163,7 +183,7 @@ hipError_t launch_egress_generic(const EgressParams& p, int dtype, hipStream_t s
 hipError_t launch_ingress_generic_impl(const IngressParams& p, int dtype, int32_t* status,
                                        hipStream_t s);
 hipError_t launch_ingress_finalize(const IngressParams& p, hipStream_t s);
-hipError_t launch_reset_fail(DeviceState* st, hipStream_t s);
+hipError_t launch_reset_call(CallState* call, hipStream_t s);
 hipError_t launch_chacha_xor(const uint8_t* src, uint8_t* dst, size_t len, ChaKey key,
                              uint32_t ctr, uint32_t n0, uint32_t n1, uint32_t n2, hipStream_t s);
 hipError_t launch_selftest(unsigned int* bad, hipStream_t s);

@@ -12,7 +12,6 @@
 
 namespace ztcp {
 
-constexpr uint32_t kSpinLimit = 1u << 20;  // about 30 ms of s_sleep(1)
 constexpr int kRowWords = 64 * 16;         // one row: 64 pages x 16 words
 
 // Word offset of quad q (16 bytes) of page `pg` inside a row slot.  The quad
@@ -50,18 +49,39 @@ __device__ __forceinline__ void lds_put_quad_at(uint32_t* row, uint32_t byte_off
     *reinterpret_cast<uint4*>(reinterpret_cast<char*>(row) + byte_off) = x;
 }
 
+// Where a wave's bounded waits report an expiry: the device's sticky
+// diagnostics, the call's own diagnostics (ingress) and an LDS word of the
+// workgroup, which the kernel reads after its last barrier to fail every
+// page of the workgroup closed.
+struct Waiter {
+    uint32_t* dev_diag;
+    uint32_t* call_diag;   // nullptr: no per-call record
+    uint32_t* expired;     // LDS
+    uint32_t spin_limit;
+};
+
+__device__ __forceinline__ Waiter make_waiter(const WaitSink& s, uint32_t* expired_lds) {
+    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit};
+}
+
 // Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
-// Bounded: an expired wait sets the sticky diagnostic bit DIAG and returns.
+// Bounded: after spin_limit polls the wait records DIAG (device and call
+// diagnostics, the workgroup's LDS word) and returns; the caller carries on,
+// and the kernel fails the workgroup's pages at its end.
 template <uint32_t DIAG>
-__device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, DeviceState* st) {
+__device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, const Waiter& w) {
     if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
     for (uint32_t spin = 0;; ++spin) {
-        __builtin_amdgcn_s_sleep(1);
-        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
-        if (spin >= kSpinLimit) {
-            atomicOr(&st->diag, DIAG);
+        if (spin >= w.spin_limit) {
+            if ((threadIdx.x & 63) == 0) {
+                atomicOr(w.dev_diag, DIAG);
+                if (w.call_diag) atomicOr(w.call_diag, DIAG);
+            }
+            __hip_atomic_store(w.expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             return;
         }
+        __builtin_amdgcn_s_sleep(1);
+        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
     }
 }
 
@@ -102,11 +122,11 @@ __device__ __forceinline__ void mac_fetch(const uint32_t* ring, const uint32_t* 
 // of this row: memory instructions spread over the chain cost it nothing,
 // while four in a row stall the wave on the address unit.
 template <uint32_t DIAG, class OnQuad>
-__device__ __forceinline__ void mac_absorb(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
+__device__ __forceinline__ void mac_absorb(const Waiter& wt, const uint32_t* ring, const uint32_t* ring_flags,
                                            uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want,
                                            bool ready, OnQuad& on_quad, const MacRow& prev, bool has_prev) {
     if (!ready) {
-        wait_ge<DIAG>(ring_flags + r.slot, want, st);
+        wait_ge<DIAG>(ring_flags + r.slot, want, wt);
 #pragma unroll
         for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
@@ -138,7 +158,7 @@ __device__ __forceinline__ bool mac_ready(const MacRow& r, int32_t want) {
 // loop begins (a scalar load in particular, as those complete out of order)
 // would turn the loop's LDS waits into full waits.
 template <int RING, uint32_t DIAG, class OnQuad>
-__device__ __forceinline__ void mac_rows(DeviceState* st, const uint32_t* ring, const uint32_t* ring_flags,
+__device__ __forceinline__ void mac_rows(const Waiter& st, const uint32_t* ring, const uint32_t* ring_flags,
                                          uint32_t* used, const PageQuads& pq, Sip& s, int32_t total,
                                          OnQuad&& on_quad) {
     MacRow r0, r1, r2;

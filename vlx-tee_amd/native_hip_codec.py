@@ -66,6 +66,10 @@ def _raise_rc(rc: int) -> None:
         return
     if rc in _MSG:
         raise RuntimeError(_MSG[rc])
+    if rc in (N.EINVAL, N.EOVERLAP):  # the reference's TORCH_CHECK message for the condition
+        raise RuntimeError(N.last_error())
+    if rc == N.EDEVICE:  # fail closed: outputs are zeroed, the batch is rejected
+        raise RuntimeError("KV_INTEGRITY_ERROR: device-side bounded wait expired; outputs zeroed")
     raise RuntimeError(f"ztcp: {N.strerror(rc)} (code {rc})")
 
 
@@ -76,9 +80,12 @@ def fused_encode_cold_pages_peak_into(
     out_blobs: torch.Tensor, preset: int, rope_mode: int, rope_dim: int,
     expected_payload_bytes: int, tenant_id_hash: int, model_id_hash: int, layer_id: int,
     head_group_id: int, base_sequence_nonce: int, k0: int, k1: int, mk0: int, mk1: int,
-    k2: int = 0, k3: int = 0,
+    k2: int = 0, k3: int = 0, *, ext_layouts: bool = False,
 ) -> None:
-    """Batch egress into a preallocated [B, blob_bytes] uint8 tensor (cpp:1904-2004)."""
+    """Batch egress into a preallocated [B, blob_bytes] uint8 tensor (cpp:1904-2004).
+
+    Presets 1..3 and RoPE modes 0..2, as the reference; ``ext_layouts`` also
+    admits this codec's extension presets 4..6 and RoPE mode 3."""
     dt = _hot_dtype(k_pages, "k_pages")
     _check(k_pages.dim() == 4, "k_pages must have shape [batch, num_tokens, num_heads, head_dim]")
     _check(out_blobs.is_cuda and out_blobs.is_contiguous() and out_blobs.dtype == torch.uint8,
@@ -93,24 +100,25 @@ def fused_encode_cold_pages_peak_into(
         _check(_hot_dtype(v_pages_opt, "v_pages") == dt and v_pages_opt.device == k_pages.device,
                "v_pages must match k_pages dtype and device")
         _check(v_pages_opt.shape == k_pages.shape, "v_pages shape must match k_pages shape")
-    # 1..3 / 0..2 are the reference's; presets 4..6 and RoPE mode 3 are this
-    # codec's extension kinds (include/ztcp.h)
-    _check(1 <= preset <= 6, "Invalid preset (must be 1..6)")
-    _check(0 <= rope_mode <= 3, "Invalid rope_mode (must be 0..3)")
+    # cpp:1947-1948; presets 4..6 and RoPE mode 3 are this codec's extension
+    # kinds (include/ztcp.h), admitted only on request
+    if ext_layouts:
+        _check(1 <= preset <= 6, "Invalid preset (must be 1..6)")
+        _check(0 <= rope_mode <= 3, "Invalid rope_mode (must be 0..3)")
+    else:
+        _check(1 <= preset <= 3, "Invalid preset (must be 1..3)")
+        _check(0 <= rope_mode <= 2, "Invalid rope_mode (must be 0..2)")
     th = _hashes_on(page_token_hashes, k_pages.device, "page_token_hashes", B)
     g = N.geometry(T, H, D, rope_dim, dt, False)
     aad = N.Aad(tenant_id_hash & 0xFFFFFFFF, model_id_hash & 0xFFFFFFFF, layer_id & 0xFFFF,
                 head_group_id & 0xFFFF)
     with torch.cuda.device(k_pages.device):
-        rc = N.lib().ztcp_egress_peak_into(
+        rc = N.lib().ztcp_egress_peak_into_ext(
             k_pages.data_ptr(), v_pages_opt.data_ptr() if v_pages_opt is not None else None,
             th.data_ptr(), out_blobs.data_ptr(), B, C.byref(g), preset, rope_mode,
             expected_payload_bytes, C.byref(aad), base_sequence_nonce & ((1 << 64) - 1),
-            C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)), _stream())
-    if rc == N.EINVAL:
-        raise RuntimeError("expected_payload_bytes smaller than required payload")
-    if rc == N.EOVERLAP:
-        raise RuntimeError("out_blobs must not alias or overlap input tensors")
+            C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)), N.EXT_LAYOUTS if ext_layouts else 0,
+            _stream())
     _raise_rc(rc)
 
 
@@ -118,7 +126,8 @@ def fused_encode_cold_pages_batch(
     k_pages: torch.Tensor, v_pages_opt: torch.Tensor | None, page_token_hashes: torch.Tensor,
     preset: int, rope_mode: int, rope_dim: int, expected_payload_bytes: int,
     tenant_id_hash: int, model_id_hash: int, layer_id: int, head_group_id: int,
-    base_sequence_nonce: int, k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0,
+    base_sequence_nonce: int, k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0, *,
+    ext_layouts: bool = False,
 ) -> torch.Tensor:
     """Allocating batch egress (cpp:1775-1902): returns [B, blob_bytes] uint8."""
     _check(k_pages.dim() == 4, "k_pages must have shape [batch, num_tokens, num_heads, head_dim]")
@@ -127,7 +136,7 @@ def fused_encode_cold_pages_batch(
     fused_encode_cold_pages_peak_into(
         k_pages, v_pages_opt, page_token_hashes, out, preset, rope_mode, rope_dim,
         expected_payload_bytes, tenant_id_hash, model_id_hash, layer_id, head_group_id,
-        base_sequence_nonce, k0, k1, mk0, mk1, k2, k3)
+        base_sequence_nonce, k0, k1, mk0, mk1, k2, k3, ext_layouts=ext_layouts)
     return out
 
 
@@ -135,7 +144,7 @@ def fused_encode_cold_page(
     k_page: torch.Tensor, v_page_opt: torch.Tensor | None, preset: int, rope_mode: int,
     rope_dim: int, expected_payload_bytes: int, tenant_id_hash: int, model_id_hash: int,
     layer_id: int, head_group_id: int, page_token_hash: int, sequence_nonce: int,
-    k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0,
+    k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0, *, ext_layouts: bool = False,
 ) -> torch.Tensor:
     """Single-page egress (cpp:1478-1555): returns a 1D uint8 blob."""
     _check(k_page.dim() == 3, "k_page must have shape [num_tokens, num_heads, head_dim]")
@@ -144,7 +153,7 @@ def fused_encode_cold_page(
     out = fused_encode_cold_pages_batch(
         k_page.unsqueeze(0), v_page_opt.unsqueeze(0) if v_page_opt is not None else None, th,
         preset, rope_mode, rope_dim, expected_payload_bytes, tenant_id_hash, model_id_hash,
-        layer_id, head_group_id, sequence_nonce, k0, k1, mk0, mk1, k2, k3)
+        layer_id, head_group_id, sequence_nonce, k0, k1, mk0, mk1, k2, k3, ext_layouts=ext_layouts)
     return out[0]
 
 
@@ -194,8 +203,6 @@ def fused_decode_cold_pages_peak_into(
             expected_tenant_hash & 0xFFFFFFFF, expected_model_hash & 0xFFFFFFFF,
             expected_layer_id & 0xFFFF, C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)), st_ptr, flags,
             _stream())
-    if rc == N.EOVERLAP:
-        raise RuntimeError("out_k_pages must not alias or overlap input tensors")
     _raise_rc(rc)
 
 
@@ -273,3 +280,9 @@ def siphash24_128(data_u8: torch.Tensor, mk0: int, mk1: int) -> torch.Tensor:
 def device_diag() -> int:
     """Sticky device diagnostics (0 = none); synchronizes the device."""
     return N.lib().ztcp_device_diag()
+
+
+def debug_spin_limit(n: int) -> int:
+    """Test hook: polls before a fused kernel's bounded wait gives up, for later
+    calls (n < 0 restores the default); returns the previous value."""
+    return N.lib().ztcp_debug_spin_limit(n)

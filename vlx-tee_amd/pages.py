@@ -51,12 +51,17 @@ def _stream() -> C.c_void_p:
 def egress(descs: torch.Tensor, n_pages: int, *, num_tokens: int, num_heads: int, head_dim: int,
            rope_dim: int, dtype: torch.dtype, is_mla_single_buffer: bool, preset: int,
            rope_mode: int, expected_payload_bytes: int, tenant_id_hash: int, model_id_hash: int,
-           k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0) -> None:
+           k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0,
+           ext_layouts: bool = False) -> None:
+    """``ext_layouts`` admits the extension presets 4..6 / RoPE mode 3."""
     g = N.geometry(num_tokens, num_heads, head_dim, rope_dim, _DTYPES[dtype], is_mla_single_buffer)
     rc = N.lib().ztcp_egress_batch(descs.data_ptr(), n_pages, C.byref(g), preset, rope_mode,
                                    expected_payload_bytes, tenant_id_hash & 0xFFFFFFFF,
                                    model_id_hash & 0xFFFFFFFF,
-                                   C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)), _stream())
+                                   C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)),
+                                   N.EXT_LAYOUTS if ext_layouts else 0, _stream())
+    if rc in (N.EINVAL, N.EOVERLAP):
+        raise RuntimeError(f"ztcp_egress_batch: {N.last_error()}")
     if rc != N.OK:
         raise RuntimeError(f"ztcp_egress_batch: {N.strerror(rc)} ({rc})")
 
@@ -79,6 +84,8 @@ def ingress(descs: torch.Tensor, n_pages: int, blob_bytes: int, *, num_tokens: i
                                     C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)),
                                     page_status.data_ptr() if page_status is not None else None,
                                     flags, _stream())
+    if rc in (N.EINVAL, N.EOVERLAP):
+        raise RuntimeError(f"ztcp_ingress_batch: {N.last_error()}")
     if rc < 0:
         raise RuntimeError(f"ztcp_ingress_batch: {N.strerror(rc)} ({rc})")
     return rc
