@@ -84,6 +84,8 @@ enum { ZTCP_HOT_FP16 = 0, ZTCP_HOT_BF16 = 1 };
 #define ZTCP_EHIP (-3)     /* the HIP runtime reported an error */
 #define ZTCP_EDEVICE (-4)  /* a kernel's bounded wait expired: outputs are zeroed
                               (see ztcp_device_diag) */
+#define ZTCP_ESCRATCH (-5) /* batch larger than ZTCP_NOALLOC_MAX_PAGES
+                              (ztcp_ingress_peak_into_noalloc only) */
 
 /* Call flags. */
 #define ZTCP_ASYNC 0x1u          /* ingress: enqueue only; verdicts land in page_status */
@@ -195,6 +197,25 @@ int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
                            uint32_t expected_tenant_hash, uint32_t expected_model_hash,
                            uint16_t expected_layer_id, const ztcp_keys* keys,
                            int32_t* page_status, uint32_t flags, void* stream);
+
+/* Ingress that allocates nothing.  No counterpart in the reference: for
+ * callers that cannot allocate device or pinned memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid it).  Same arguments,
+ * checks, kernels and results as ztcp_ingress_peak_into; the call's device
+ * state (failure word, diagnostics, and the per-page status array the
+ * generic kernels need when page_status is NULL) lives in a fixed device
+ * array of about 256 KiB that each GPU holds until the process ends, so
+ * batches are limited to ZTCP_NOALLOC_MAX_PAGES pages (ZTCP_ESCRATCH beyond).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialized by the caller.
+ * The array is set up on the first call on each device. */
+#define ZTCP_NOALLOC_MAX_PAGES 65536
+int ztcp_ingress_peak_into_noalloc(const uint8_t* cold_blobs, int64_t blob_bytes,
+                                   const int64_t* expected_token_hashes, void* out_k_pages,
+                                   void* out_v_pages, int64_t batch, const ztcp_geometry* g,
+                                   uint32_t expected_tenant_hash, uint32_t expected_model_hash,
+                                   uint16_t expected_layer_id, const ztcp_keys* keys,
+                                   int32_t* page_status, uint32_t flags, void* stream);
 
 /* Descriptor form of the same ingress (blob in, k/v out; the expected token
  * hash and layer id of each page come from its descriptor). */

@@ -16,7 +16,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libztcp_hip.so"
 
 # Return codes (include/ztcp.h).
 OK, ERR_HEADER, ERR_AAD, ERR_MAC, ERR_DEVICE = 0, 1, 2, 3, 4
-EINVAL, EOVERLAP, EHIP, EDEVICE = -1, -2, -3, -4
+EINVAL, EOVERLAP, EHIP, EDEVICE, ESCRATCH = -1, -2, -3, -4, -5
+NOALLOC_MAX_PAGES = 65536
 ASYNC, PER_PAGE, EXT_LAYOUTS = 0x1, 0x2, 0x4
 HOT_FP16, HOT_BF16 = 0, 1
 
@@ -24,7 +25,7 @@ HOT_FP16, HOT_BF16 = 0, 1
 EXPORTS = (
     "ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes",
     "ztcp_egress_peak_into", "ztcp_egress_peak_into_ext", "ztcp_egress_batch",
-    "ztcp_ingress_peak_into", "ztcp_ingress_batch",
+    "ztcp_ingress_peak_into", "ztcp_ingress_peak_into_noalloc", "ztcp_ingress_batch",
     "ztcp_chacha20_xor", "ztcp_siphash128",
     "ztcp_selftest", "ztcp_device_diag", "ztcp_debug_spin_limit", "ztcp_strerror",
     "ztcp_last_error",
@@ -95,6 +96,8 @@ def lib() -> C.CDLL:
     L.ztcp_egress_batch.restype = i32
     L.ztcp_ingress_peak_into.argtypes = [P, i64, P, P, P, i64, G, u32, u32, u16, K, P, u32, P]
     L.ztcp_ingress_peak_into.restype = i32
+    L.ztcp_ingress_peak_into_noalloc.argtypes = [P, i64, P, P, P, i64, G, u32, u32, u16, K, P, u32, P]
+    L.ztcp_ingress_peak_into_noalloc.restype = i32
     L.ztcp_ingress_batch.argtypes = [P, i64, i64, G, u32, u32, K, P, u32, P]
     L.ztcp_ingress_batch.restype = i32
     L.ztcp_chacha20_xor.argtypes = [P, P, C.c_size_t, P, u32, P, P]

@@ -219,10 +219,19 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
     return e == hipSuccess ? ZTCP_OK : ZTCP_EHIP;
 }
 
-int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok, void* out_k,
-                   void* out_v, const ztcp_page_desc* descs, int64_t batch, const ztcp_geometry* g,
-                   uint32_t tenant, uint32_t model, uint16_t layer, const ztcp_keys* keys,
-                   int32_t* page_status, uint32_t flags, hipStream_t stream) {
+// An ingress call's validated parameters: the reference's argument checks
+// (cpp:2267-2296) and the kernel argument block, without any device state.
+struct IngressCall {
+    IngressParams p{};
+    int dtype = 0;
+    bool fast = false;
+    bool async = false;
+};
+
+int ingress_prepare(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok, void* out_k, void* out_v,
+                    const ztcp_page_desc* descs, int64_t batch, const ztcp_geometry* g, uint32_t tenant,
+                    uint32_t model, uint16_t layer, const ztcp_keys* keys, int32_t* page_status, uint32_t flags,
+                    int cu_count, IngressCall* out) {
     t_last_error = "";
     int rc = check_geometry(g, batch, "Invalid out_k_pages dimensions");
     if (rc) return rc;
@@ -246,11 +255,8 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
         if (!mla && (overlap(out_v, kn, blobs, bn) || overlap(out_v, kn, tok, 8 * batch)))  // cpp:2293-2294
             return fail_arg(ZTCP_EOVERLAP, "out_v_pages must not alias or overlap input tensors");
     }
-    DeviceCtx* ctx = nullptr;
-    rc = device_ctx(&ctx);
-    if (rc) return rc;
-
-    IngressParams p{};
+    IngressParams& p = out->p;
+    p = IngressParams{};
     p.blobs = blobs;
     p.token_hashes = tok;
     p.out_k = (uint8_t*)out_k;
@@ -285,45 +291,117 @@ int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok,
     p.exp_model = model;
     p.exp_layer = layer;
     p.per_page = (flags & ZTCP_PER_PAGE) ? 1 : 0;
-    p.ppw = pages_per_group(batch, ctx->cu_count);
-    const bool async = (flags & ZTCP_ASYNC) != 0;
-    const bool fast = all_aligned && blob_bytes % 16 == 0 &&
-                      (descs || (aligned16(blobs) && aligned16(out_k) && (mla || aligned16(out_v))));
+    p.ppw = pages_per_group(batch, cu_count);
     p.n_units = (int32_t)(vecs * (g->head_dim / 16) * (mla ? 1 : 2));  // generic path: groups per page
+    out->dtype = g->hot_dtype;
+    out->async = (flags & ZTCP_ASYNC) != 0;
+    out->fast = all_aligned && blob_bytes % 16 == 0 &&
+                (descs || (aligned16(blobs) && aligned16(out_k) && (mla || aligned16(out_v))));
+    return ZTCP_OK;
+}
 
-    int slot = 0;
-    rc = acquire_call(ctx, &slot);
-    if (rc) return rc;
-    p.call = ctx->calls + slot;
-    p.sink = wait_sink(ctx, p.call);
-    // The generic path needs every page's status between its kernels; without
-    // the caller's array it takes a stream-ordered allocation of its own.
-    int32_t* status = page_status;
+// Enqueues an ingress call whose CallState is `call`: reset, kernels,
+// finalize, and for a synchronous call the verdict's read-back into
+// `result`.  `status` is the per-page status array of the generic path when
+// the caller gave none (nullptr: a stream-ordered allocation of its own).
+hipError_t ingress_enqueue(IngressCall& c, CallState* call, int32_t* status, const WaitSink& sink,
+                           CallState* result, hipStream_t stream) {
+    IngressParams& p = c.p;
+    p.call = call;
+    p.sink = sink;
+    if (p.page_status) status = p.page_status;
     bool own_status = false;
-    hipError_t e = launch_reset_call(p.call, stream);
-    if (e == hipSuccess && !fast && !status) {
-        e = hipMallocAsync((void**)&status, (size_t)batch * sizeof(int32_t), stream);
+    hipError_t e = launch_reset_call(call, stream);
+    if (e == hipSuccess && !c.fast && !status) {
+        e = hipMallocAsync((void**)&status, (size_t)p.batch * sizeof(int32_t), stream);
         own_status = e == hipSuccess;
     }
     if (e == hipSuccess) {
-        e = fast ? launch_ingress_fused(p, g->hot_dtype, stream)
-                 : launch_ingress_generic_impl(p, g->hot_dtype, status, stream);
-        if (e == hipSuccess && fast && !p.per_page) e = launch_ingress_finalize(p, stream);
+        e = c.fast ? launch_ingress_fused(p, c.dtype, stream) : launch_ingress_generic_impl(p, c.dtype, status, stream);
+        if (e == hipSuccess && c.fast && !p.per_page) e = launch_ingress_finalize(p, stream);
     }
     if (own_status && hipFreeAsync(status, stream) != hipSuccess && e == hipSuccess) e = hipErrorUnknown;
-    if (e == hipSuccess && !async)
-        e = hipMemcpyAsync(ctx->host_calls + slot, p.call, sizeof(CallState), hipMemcpyDeviceToHost, stream);
-    if (e == hipSuccess && !async) e = hipStreamSynchronize(stream);
-    // read the verdict while the slot (and its read-back area) is still ours
-    const CallState r = (e == hipSuccess && !async) ? ctx->host_calls[slot] : CallState{~0ull, 0u, 0u};
-    // a failed launch leaves the slot to an event, as the kernels before it
-    // may still run
-    const int rel = release_call(ctx, slot, stream, async || e != hipSuccess);
-    if (e != hipSuccess) return ZTCP_EHIP;
-    if (rel) return rel;
-    if (async) return ZTCP_OK;
+    if (e == hipSuccess && !c.async) e = hipMemcpyAsync(result, call, sizeof(CallState), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess && !c.async) e = hipStreamSynchronize(stream);
+    return e;
+}
+
+int verdict(const CallState& r) {
     if (r.diag) return ZTCP_EDEVICE;
     return r.fail == ~0ull ? ZTCP_OK : (int)(r.fail & 0xFFu);
+}
+
+int ingress_common(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok, void* out_k,
+                   void* out_v, const ztcp_page_desc* descs, int64_t batch, const ztcp_geometry* g,
+                   uint32_t tenant, uint32_t model, uint16_t layer, const ztcp_keys* keys,
+                   int32_t* page_status, uint32_t flags, hipStream_t stream) {
+    DeviceCtx* ctx = nullptr;
+    IngressCall c;
+    int rc = ingress_prepare(blobs, blob_bytes, tok, out_k, out_v, descs, batch, g, tenant, model, layer, keys,
+                             page_status, flags, 0, &c);
+    if (rc) return rc;
+    rc = device_ctx(&ctx);
+    if (rc) return rc;
+    c.p.ppw = pages_per_group(batch, ctx->cu_count);
+    int slot = 0;
+    rc = acquire_call(ctx, &slot);
+    if (rc) return rc;
+    CallState* call = ctx->calls + slot;
+    const hipError_t e = ingress_enqueue(c, call, nullptr, wait_sink(ctx, call), ctx->host_calls + slot, stream);
+    // read the verdict while the slot (and its read-back area) is still ours
+    const CallState r = (e == hipSuccess && !c.async) ? ctx->host_calls[slot] : CallState{~0ull, 0u, 0u};
+    // a failed launch leaves the slot to an event, as the kernels before it
+    // may still run
+    const int rel = release_call(ctx, slot, stream, c.async || e != hipSuccess);
+    if (e != hipSuccess) return ZTCP_EHIP;
+    if (rel) return rel;
+    return c.async ? ZTCP_OK : verdict(r);
+}
+
+// ---------------------------------------------------------------------------
+// Ingress without allocation (ztcp_ingress_peak_into_noalloc): the call's
+// device state lives in `scratch`, a file-scope device array each GPU holds
+// one copy of until the process ends, instead of the per-device slot pool
+// and the stream-ordered status allocation.
+//   [0, 16)                      CallState (failure word, diagnostics)
+//   [16, 32)                     DeviceState (sticky diagnostics of this path)
+//   [256, 256 + 4 * kNoAllocPages)  per-page status of the generic path
+// Every call on a GPU uses the same array: calls that overlap on one GPU
+// race, and the array keeps the last call's contents (the call state is
+// reset by the call's first kernel).
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocPages = ZTCP_NOALLOC_MAX_PAGES;
+constexpr size_t kScratchStatusOff = 256;
+constexpr size_t kScratchBytes = kScratchStatusOff + sizeof(int32_t) * (size_t)kNoAllocPages;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static_assert(sizeof(CallState) == 16 && sizeof(DeviceState) == 16, "scratch layout");
+
+constexpr int kMaxDevices = 64;
+struct NoAllocDevice {
+    unsigned char* scratch = nullptr;  // this device's copy of `scratch` (hipGetSymbolAddress)
+    int cu_count = 0;
+};
+NoAllocDevice g_noalloc[kMaxDevices];
+std::mutex g_noalloc_mu;
+
+// Once per device, with that device current: the device address of its copy
+// of `scratch`.  The array's name is a host-side stand-in, never passed to a
+// kernel or copy; only this address is.
+int noalloc_device(NoAllocDevice** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ZTCP_EHIP;
+    if (dev < 0 || dev >= kMaxDevices) return fail_arg(ZTCP_EINVAL, "device index out of range for the no-allocation path");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    NoAllocDevice& d = g_noalloc[dev];
+    if (!d.scratch) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return ZTCP_EHIP;
+        if (hipDeviceGetAttribute(&d.cu_count, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return ZTCP_EHIP;
+        d.scratch = (unsigned char*)ptr;
+    }
+    *out = &d;
+    return ZTCP_OK;
 }
 
 }  // namespace
@@ -398,6 +476,32 @@ int ztcp_ingress_batch(const ztcp_page_desc* pages, int64_t n_pages, int64_t blo
                           (hipStream_t)stream);
 }
 
+int ztcp_ingress_peak_into_noalloc(const uint8_t* cold_blobs, int64_t blob_bytes,
+                                   const int64_t* expected_token_hashes, void* out_k_pages, void* out_v_pages,
+                                   int64_t batch, const ztcp_geometry* g, uint32_t expected_tenant_hash,
+                                   uint32_t expected_model_hash, uint16_t expected_layer_id,
+                                   const ztcp_keys* keys, int32_t* page_status, uint32_t flags, void* stream) {
+    if (batch > kNoAllocPages)
+        return fail_arg(ZTCP_ESCRATCH, "batch exceeds ZTCP_NOALLOC_MAX_PAGES (the no-allocation scratch capacity)");
+    IngressCall c;
+    int rc = ingress_prepare(cold_blobs, blob_bytes, expected_token_hashes, out_k_pages, out_v_pages, nullptr, batch,
+                             g, expected_tenant_hash, expected_model_hash, expected_layer_id, keys, page_status,
+                             flags, 0, &c);
+    if (rc) return rc;
+    NoAllocDevice* d = nullptr;
+    rc = noalloc_device(&d);
+    if (rc) return rc;
+    c.p.ppw = pages_per_group(batch, d->cu_count);
+    CallState* call = reinterpret_cast<CallState*>(d->scratch);
+    DeviceState* sticky = reinterpret_cast<DeviceState*>(d->scratch + sizeof(CallState));
+    int32_t* status = reinterpret_cast<int32_t*>(d->scratch + kScratchStatusOff);
+    CallState result{~0ull, 0u, 0u};  // pageable: the read-back allocates nothing
+    const WaitSink sink{&sticky->diag, &call->diag, g_spin_limit.load(std::memory_order_relaxed)};
+    const hipError_t e = ingress_enqueue(c, call, status, sink, &result, (hipStream_t)stream);
+    if (e != hipSuccess) return ZTCP_EHIP;
+    return c.async ? ZTCP_OK : verdict(result);
+}
+
 int ztcp_chacha20_xor(const uint8_t* src, uint8_t* dst, size_t len, const uint8_t key[32],
                       uint32_t initial_counter, const uint8_t nonce[12], void* stream) {
     if (!key || !nonce || (len && (!src || !dst))) return ZTCP_EINVAL;
@@ -440,13 +544,28 @@ int ztcp_device_diag(void) {
     DeviceCtx* ctx = nullptr;
     int rc = device_ctx(&ctx);
     if (rc) return rc;
-    uint32_t d = 0;
     if (hipDeviceSynchronize() != hipSuccess) return ZTCP_EHIP;
-    if (hipMemcpy(&d, &ctx->state->diag, sizeof d, hipMemcpyDeviceToHost) != hipSuccess) return ZTCP_EHIP;
-    const uint32_t zero = 0;
-    if (hipMemcpy(&ctx->state->diag, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess)
-        return ZTCP_EHIP;
-    return (int)d;
+    // the library's sticky word, and the no-allocation path's when that path
+    // has been used on this device
+    uint32_t* words[2] = {&ctx->state->diag, nullptr};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ZTCP_EHIP;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        if (dev < kMaxDevices && g_noalloc[dev].scratch)
+            words[1] = &reinterpret_cast<DeviceState*>(g_noalloc[dev].scratch + sizeof(CallState))->diag;
+    }
+    uint32_t all = 0;
+    for (uint32_t* w : words) {
+        if (!w) continue;
+        uint32_t d = 0;
+        const uint32_t zero = 0;
+        if (hipMemcpy(&d, w, sizeof d, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(w, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess)
+            return ZTCP_EHIP;
+        all |= d;
+    }
+    return (int)all;
 }
 
 int64_t ztcp_debug_spin_limit(int64_t n) {
@@ -465,6 +584,7 @@ const char* ztcp_strerror(int code) {
         case ZTCP_EOVERLAP: return "outputs must not alias or overlap input tensors";
         case ZTCP_EHIP: return "HIP runtime error";
         case ZTCP_EDEVICE: return "device-side bounded wait expired; outputs zeroed";
+        case ZTCP_ESCRATCH: return "batch exceeds ZTCP_NOALLOC_MAX_PAGES";
         default: return "unknown error";
     }
 }
