@@ -13,11 +13,13 @@ the model follows the constants the kernels are built with.
 
   egress (vlx-tee_amd/csrc/ztcp_egress.hip): producers take code rows in
     order, stage scales per unit, write the ring at the row's payload
-    position; the wave that stages a unit's last code row makes the unit's
-    scale row; a feeder copies each stored scale row into the ring at its
-    payload position; the MAC wave absorbs rows in payload order; a storer
-    wave stores every code row from the ring in payload order; a slot is
-    rewritten only once both the MAC wave and the storer have passed it.
+    position; a storer wave stores every code row from the ring in payload
+    order and, after a unit's last code row, makes the unit's scale row (its
+    staging slot is then free), publishing that scale rows are stored before
+    it next waits for a row or once four are outstanding; a feeder copies
+    each stored scale row into the ring at its payload position; the MAC
+    wave absorbs rows in payload order; a slot is rewritten only once both
+    the MAC wave and the storer have passed it.
   ingress (vlx-tee_amd/csrc/ztcp_ingress.hip): decoders take tasks in order
     (a unit's scale row two units ahead of its code rows), write code rows
     into the ring, stage decrypted scales; a feeder copies every other
@@ -40,7 +42,7 @@ def _const(fname, name):
 
 
 NBLK = {"i8": 8, "i4": 4, "raw": 16}
-LATE_SCALE_PUBLISH = False  # planted mistake: publish a stored scale row after the row's staging wait
+LAZY_SCALE_ONLY_AT_END = False  # planted mistake: the storer publishes stored scale rows only when it is done
 IGNORE_STORER = False       # planted mistake: reuse a ring slot once the MAC wave alone has passed it
 CONFIGS = {  # sections (kind, units) of the layouts the kernels meet
     "k8v4": [("i8", 16), ("i8", 16), ("i4", 32)],
@@ -120,30 +122,17 @@ def egress_model(secs, n_prod, seed):
 
     def slot_free(m):
         return st["used"] >= m - KRING + 1 and (IGNORE_STORER or st["stored"] >= m - KRING + 1)
-    stage_flag, count = [0] * KSTAGE, [0] * KSTAGE
+    stage_flag = [0] * KSTAGE
     stage_units = [None] * KSTAGE
     staged, stored = {}, set()
-
-    def make_scale(g):
-        assert staged.get(g, 0) == per_unit[g]
-        assert stage_units[g % KSTAGE] == g
-        count[g % KSTAGE] = 0
-        stage_flag[g % KSTAGE] = g + 1
 
     def producer():
         t = st["task"]; st["task"] += 1
         yield "ok"
-        owed = None
         while t < len(code):
             tn = st["task"]; st["task"] += 1
             yield "ok"
             c = code[t]
-            if owed is not None:  # scale row made and published before the row's waits
-                make_scale(owed)
-                yield "ok"
-                if not LATE_SCALE_PUBLISH:
-                    stored.add(owed)
-                    yield "ok"
             if c["quant"]:
                 g = c["g"]
                 yield from wait(lambda: stage_flag[g % KSTAGE] >= g - KSTAGE + 1)
@@ -152,9 +141,6 @@ def egress_model(secs, n_prod, seed):
                 assert stage_units[g % KSTAGE] == g, "staging slot still holds another unit"
                 staged[g] = staged.get(g, 0) + 1
                 yield "ok"
-            if owed is not None and LATE_SCALE_PUBLISH:
-                stored.add(owed)
-                yield "ok"
             m = c["m"]
             yield from wait(lambda: slot_free(m))
             assert ring_flag[m % KRING] <= max(0, m - KRING + 1), "ring slot overwritten before use"
@@ -162,18 +148,35 @@ def egress_model(secs, n_prod, seed):
             yield "ok"
             ring_flag[m % KRING] = m + 1
             yield "ok"
-            owed = None
-            if c["quant"]:
-                g = c["g"]
-                old = count[g % KSTAGE]; count[g % KSTAGE] += 1
-                yield "ok"
-                if old == c["nblk"] - 1:
-                    owed = g
             t = tn
-        if owed is not None:
-            make_scale(owed)
-            stored.add(owed)
+
+    def storer():
+        made, pub = [], 0
+        for m in range(len(prow)):
+            if prow[m][0] == "code":
+                if pub < len(made) and ring_flag[m % KRING] < m + 1 and not LAZY_SCALE_ONLY_AT_END:
+                    stored.update(made[pub:]); pub = len(made)  # published before waiting
+                    yield "ok"
+                yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
+                yield "ok"  # the slot's quads are read ...
+                assert ring[m % KRING] == prow[m], ("storer read an overwritten slot", m, ring[m % KRING])
+            st["stored"] = m + 1  # ... before the release that frees it
             yield "ok"
+            if prow[m][0] == "code":
+                _, si, u, j = prow[m]
+                kind = secs[si][0]
+                if kind != "raw" and j == NBLK[kind] - 1:
+                    g = code[[c["m"] for c in code].index(m)]["g"]
+                    assert staged.get(g, 0) == per_unit[g], "scale row made before its unit was staged"
+                    assert stage_units[g % KSTAGE] == g
+                    stage_flag[g % KSTAGE] = g + 1
+                    made.append(g)
+                    yield "ok"
+                    if len(made) - pub >= 4 and not LAZY_SCALE_ONLY_AT_END:
+                        stored.update(made[pub:]); pub = len(made)
+                        yield "ok"
+        stored.update(made[pub:])
+        yield "ok"
 
     def feeder():
         # scale rows in payload order; within a section the next row's load
@@ -199,15 +202,6 @@ def egress_model(secs, n_prod, seed):
             yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
             assert ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m])
             st["used"] = m + 1
-            yield "ok"
-
-    def storer():  # code rows only; scale rows are stored by their makers
-        for m in range(len(prow)):
-            if prow[m][0] == "code":
-                yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
-                yield "ok"  # the slot's quads are read ...
-                assert ring[m % KRING] == prow[m], ("storer read an overwritten slot", m, ring[m % KRING])
-            st["stored"] = m + 1  # ... before the release that frees it
             yield "ok"
 
     return Sched(seed).run([producer() for _ in range(n_prod)] + [feeder(), mac(), storer()])
@@ -327,16 +321,16 @@ def test_ingress_handoffs(cfg, waves):
         assert ingress_model(CONFIGS[cfg], waves, seed + 100, padding=5)
 
 
-def test_egress_model_catches_a_late_scale_publication():
-    """A planted mistake: a wave that publishes its scale row only after its
-    next row's staging wait can hold up the feeder while it waits; with
-    enough waves in flight the model finds the deadlock."""
-    global LATE_SCALE_PUBLISH
-    LATE_SCALE_PUBLISH = True
+def test_egress_model_catches_scale_rows_published_only_at_the_end():
+    """A planted mistake: a storer that publishes its stored scale rows only
+    when it is done holds up the feeder, through it the MAC wave, and through
+    the ring the producers whose rows the storer waits for: a deadlock."""
+    global LAZY_SCALE_ONLY_AT_END
+    LAZY_SCALE_ONLY_AT_END = True
     try:
-        assert not all(egress_model(CONFIGS["k8v4"], 48, seed) for seed in range(5))
+        assert not all(egress_model(CONFIGS["k8v4"], 12, seed) for seed in range(5))
     finally:
-        LATE_SCALE_PUBLISH = False
+        LAZY_SCALE_ONLY_AT_END = False
 
 
 def test_egress_model_catches_a_slot_reused_before_the_storer_read_it():

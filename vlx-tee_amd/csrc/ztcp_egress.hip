@@ -64,8 +64,7 @@ constexpr int kScaleSlots = 64;       // scale rows the feeder wave may still be
 constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
 constexpr int kFlagRing = 0;                          // [kRing] MAC row index + 1
 constexpr int kFlagStage = kFlagRing + kRing;         // [kStage] unit + 1: staging slot free
-constexpr int kFlagCount = kFlagStage + kStage;       // [kStage] code rows staged in the slot
-constexpr int kFlagScale = kFlagCount + kStage;       // [kScaleSlots] unit + 1: scale row stored
+constexpr int kFlagScale = kFlagStage + kStage;       // [kScaleSlots] unit + 1: scale row stored
 constexpr int kFlagMacUsed = kFlagScale + kScaleSlots;  // rows absorbed by the MAC wave
 constexpr int kFlagStored = kFlagMacUsed + 1;         // rows passed by the storer wave
 constexpr int kFlagTask = kFlagStored + 1;            // next code row to hand out
@@ -232,25 +231,18 @@ __device__ __forceinline__ uint32_t quant_half_int4g32(const uint32_t (&w)[4][8]
     return sa | (sbb << 16);
 }
 
-// Publishes that scale row g is in the blobs, for the MAC wave to read.
-__device__ __forceinline__ void publish_scale(uint32_t* flags, int32_t g) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    publish(&flags[kFlagScale + g % kScaleSlots], (uint32_t)g + 1u);
-}
-
-// The scale row of row.u's unit, run by the wave that staged the unit's last
-// scales, during its next code row (after that row's groups have arrived):
-// encrypts the staged scales in place and stores the block.  Frees the
-// staging slot at once; the stores' completion is published later
-// (publish_scale) so that the wave does not wait for them here.
-__device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) {
+// The scale row of unit g (payload block `block`), made by the storer wave
+// once it has stored the unit's last code row: every code row of the unit
+// stages its scales before it releases its ring row, so all of them are in
+// the staging slot by then.  Encrypts the staged scales in place, stores the
+// block transposed and frees the staging slot; that the stores have
+// completed is published later (publish_scales).
+__device__ __forceinline__ void scale_row(const ProducerCtx& c, int32_t g, uint32_t block) {
     const EgressParams& p = *c.p;
     uint32_t* flags = c.lds + kLdsFlags;
-    const uint32_t block = row.s.s_off / 64u + (uint32_t)row.u;
     uint32_t ks[16];
     chacha_block_cached(p.key, c.nc, 1u + block, c.n0, c.n1, c.n2, ks);
-    uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
+    uint32_t* stage = c.lds + kLdsStage + (g % kStage) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint4 s = lds_quad(stage, c.lane, q);
@@ -258,29 +250,29 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, const Row& row) 
                      make_uint4(s.x ^ ks[4 * q], s.y ^ ks[4 * q + 1], s.z ^ ks[4 * q + 2], s.w ^ ks[4 * q + 3]));
     }
     store_row(stage, c, (uint32_t)kHeader + 64u * block);
-    flags[kFlagCount + row.g % kStage] = 0u;
-    publish(&flags[kFlagStage + row.g % kStage], (uint32_t)row.g + 1u);
+    publish(&flags[kFlagStage + g % kStage], (uint32_t)g + 1u);  // the release follows the slot reads
 }
 
-// One code row.  w holds the row's first four chunks, loaded a row ahead;
-// an int4 (or int4 per 32) row loads its second four into w once the first
-// four are quantized, and uses them after four double rounds.  Every kind of row
-// issues the next row's loads at the same point, into the same registers,
-// so that no path has to move a register whose load is still in flight
-// (such a move would make the wave wait for it).  A scale row this wave owes
-// (the last code row of a unit it staged) is made right after this row's
-// groups have arrived and published before this row's only wait that
-// depends on the MAC wave.
+// Publishes that scale rows [from, to) are in the blobs, for the feeder.
+__device__ __forceinline__ void publish_scales(uint32_t* flags, int32_t from, int32_t to) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+#pragma unroll 1
+    for (int32_t g = from; g < to; ++g) publish(&flags[kFlagScale + g % kScaleSlots], (uint32_t)g + 1u);
+}
+
+// Whether a row of this kind quantizes eight 16-element chunks (int4, int4 per
+// 32): those rows load their chunks in two halves of four.
+template <int FAM>
+__device__ __forceinline__ bool two_halves(int32_t kind) {
+    return kind == kSecInt4 || (FAM == 1 && kind == kSecInt4G32);
+}
+
+// Quantizes a row's first four chunks (w) into pt[] and its parameter words
+// into sc[] (raw rows copy their two chunks).
 template <int DT, int FAM>
-__device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt,
-                                         uint32_t (&w)[4][8], const Row& unit_done, bool make_scale) {
-    const EgressParams& p = *c.p;
-    uint32_t* flags = c.lds + kLdsFlags;
-    const int32_t kind = row.s.kind;
-    uint32_t pt[16];
-    uint32_t sc[4];
-    ChaChaState st;
-    st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
+__device__ __forceinline__ void quant_first(int32_t kind, const uint32_t (&w)[4][8], uint32_t (&pt)[16],
+                                            uint32_t (&sc)[4]) {
     if (kind == kSecInt8) {
         quant_half<DT, 8>(w, pt, sc);
     } else if (kind == kSecInt4) {
@@ -296,16 +288,39 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         else if (kind == kSecInt4G32) sc[0] = quant_half_int4g32<DT>(w, pt);
         else sc[0] = quant_group64_asym8<DT>(w, pt);
     }
-    const bool two_halves = kind == kSecInt4 || (FAM == 1 && kind == kSecInt4G32);
-    if (two_halves) load_half(p, c.pg, row, 1, w);
-    if (make_scale) scale_row(c, unit_done);
+}
+
+// The first half of a row's chunks: loads them, and once they have arrived
+// quantizes them and issues the loads of the second half (rows of eight
+// chunks), which then arrive during the row's first double rounds.  Run at
+// the end of the previous row, whose last rounds cover the first half's
+// loads.
+template <int DT, int FAM>
+__device__ __forceinline__ void first_half(const EgressParams& p, const EgressPage& pg, const Row& row,
+                                           uint32_t (&w)[4][8], uint32_t (&pt)[16], uint32_t (&sc)[4]) {
+    quant_first<DT, FAM>(row.s.kind, w, pt, sc);
+    if (two_halves<FAM>(row.s.kind)) load_half(p, pg, row, 1, w);
+}
+
+// One code row.  pt / sc hold the row's first half quantized (first_half, at
+// the end of the previous row) and w the second half's chunks when the row
+// has two, loaded since; the second half is quantized after four double
+// rounds.  The next row's first four chunks are loaded into w then, and at
+// the end of this row first_half runs for the next row.  Every kind of row
+// issues the next row's loads at the same point, into the same registers,
+// so that no path has to move a register whose load is still in flight
+// (such a move would make the wave wait for it).
+template <int DT, int FAM>
+__device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, const Row& nxt,
+                                         uint32_t (&w)[4][8], uint32_t (&pt)[16], uint32_t (&sc)[4]) {
+    const EgressParams& p = *c.p;
+    uint32_t* flags = c.lds + kLdsFlags;
+    const int32_t kind = row.s.kind;
+    ChaChaState st;
+    st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
     st.double_rounds<4>();
     if (kind == kSecInt4) quant_half<DT, 4>(w, pt + 8, sc + 2);
     else if (FAM == 1 && kind == kSecInt4G32) sc[1] = quant_half_int4g32<DT>(w, pt + 8);
-    // the scale row's stores were issued four double rounds ago; publishing
-    // them before any wait of this row keeps the feeder (and through it the
-    // MAC wave) from depending on this row's waits
-    if (make_scale) publish_scale(flags, unit_done.g);
     if (nxt.valid) load_half(p, c.pg, nxt, 0, w);
     st.double_rounds<5>();
     if (kind != kSecRaw) {
@@ -323,15 +338,21 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     }
     uint32_t ks[16];
     st.finish(p.key, 1u + (uint32_t)row.block, c.n0, c.n1, c.n2, ks);
+    // the row's ciphertext is complete before the ring waits: left to
+    // itself, the compiler sinks the last rounds below the waits (their
+    // results are only used after them), so a wave that finds the ring full
+    // would wait first and compute afterwards
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ks[i] ^= pt[i];
+    pin_words(ks);
     uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
     wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, c.wt);
     wait_ge<kDiagEgressWait>(&flags[kFlagStored], row.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        lds_put_quad(slot, c.lane, q,
-                     make_uint4(pt[4 * q] ^ ks[4 * q], pt[4 * q + 1] ^ ks[4 * q + 1],
-                                pt[4 * q + 2] ^ ks[4 * q + 2], pt[4 * q + 3] ^ ks[4 * q + 3]));
+        lds_put_quad(slot, c.lane, q, make_uint4(ks[4 * q], ks[4 * q + 1], ks[4 * q + 2], ks[4 * q + 3]));
     publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);  // the storer wave stores it
+    if (nxt.valid) first_half<DT, FAM>(p, c.pg, nxt, w, pt, sc);
 }
 
 template <int DT, int FAM>
@@ -346,7 +367,6 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
     c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
-    c.init_stores(ppw);
     const int32_t total = total_code_rows(p.lay);
     // The page descriptor and kernel argument loads above complete here,
     // before the loop: a load still counted as in flight where the loop
@@ -357,43 +377,32 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     // code rows are handed out in order from an LDS counter, one row ahead of
     // the one being made (so its groups can be prefetched): a slower wave
     // simply takes fewer rows
+    // (also reads how many rows the MAC wave has absorbed, for the priority)
+    int32_t used = 0;
     auto grab = [&]() -> int32_t {
         uint32_t t = 0;
+        const uint32_t u = __hip_atomic_load(&flags[kFlagMacUsed], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (c.lane == 0)
             t = __hip_atomic_fetch_add(&flags[kFlagTask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        used = (int32_t)__builtin_amdgcn_readfirstlane(u);
         return (int32_t)__builtin_amdgcn_readfirstlane(t);
     };
     uint32_t w[4][8];
-    Row unit_done{};         // unit whose last code row this wave staged
-    bool make_scale = false;  // its scale row is still to be made
+    uint32_t pt[16], sc[4];
     int32_t t = grab();
     Row cur = row_info(p.lay, t);
-    if (cur.valid) load_half(p, c.pg, cur, 0, w);
+    if (cur.valid) {
+        load_half(p, c.pg, cur, 0, w);
+        first_half<DT, FAM>(p, c.pg, cur, w, pt, sc);
+    }
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
+        set_row_priority(cur.mrow - used);
         const Row nxt = row_info(p.lay, tn);
-        code_row<DT, FAM>(c, cur, nxt, w, unit_done, make_scale);
-        make_scale = false;
-        if (cur.s.kind != kSecRaw) {
-            // count the unit's staged code rows; whoever stages the last one
-            // encrypts the unit's scales (during its next row)
-            uint32_t old = 0;
-            if (c.lane == 0)
-                old = __hip_atomic_fetch_add(&flags[kFlagCount + cur.g % kStage], 1u, __ATOMIC_ACQ_REL,
-                                             __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __builtin_amdgcn_readfirstlane(old);
-            if (old == (uint32_t)cur.s.nblk - 1u) {
-                unit_done = cur;
-                make_scale = true;
-            }
-        }
+        code_row<DT, FAM>(c, cur, nxt, w, pt, sc);
         t = tn;
         cur = nxt;
-    }
-    if (make_scale) {
-        scale_row(c, unit_done);
-        publish_scale(flags, unit_done.g);
     }
 }
 
@@ -526,42 +535,80 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
     }
 }
 
-// FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also the
-// extension kinds (e4m3, int4 per 32, asym8).  Separate instantiations keep
-// the extension's registers out of the reference kinds' kernel.
 // Storer (one wave on SIMD 1): stores every code row from the ring to the
 // blobs, in payload order (the MAC order), transposed -- four lanes per page,
 // 64 contiguous bytes of 16 pages per store instruction -- and publishes
 // `stored` = rows passed; a ring slot is rewritten only once the MAC wave and
-// the storer have both passed it.  Scale rows are skipped: their makers store
-// them.  Stores are kept off the producers, whose waits for their own loads
-// would otherwise also wait for every store they issued before those loads,
-// and off the MAC wave's SIMD, where the data and address reads of scattered
-// stores take register-file cycles from the chain.  The storer issues no
-// loads, so it never waits for its stores.
+// the storer have both passed it.  Once it has stored a unit's last code row
+// it also makes the unit's scale row (every code row stages its scales before
+// releasing its ring row), so the producers never wait for a unit to fill.
+// That a scale row's stores have completed is published for the feeder
+// before the storer next waits for a row, or once four are outstanding: the
+// storer issues no loads, so those waits only cover its own stores.  Stores
+// are kept off the producers, whose waits for their own loads would
+// otherwise also wait for every store they issued before those loads, and
+// off the MAC wave's SIMD, where the data and address reads of scattered
+// stores take register-file cycles from the chain.
 __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
     ProducerCtx c;
     c.p = &p;
     c.lane = threadIdx.x & 63;
+    c.pg = egress_page(p, page0 + (c.lane < ppw ? c.lane : 0));
+    c.n0 = (uint32_t)c.pg.seq;
+    c.n1 = (uint32_t)(c.pg.seq >> 32);
+    c.n2 = c.pg.nonce2;
+    c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
     c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
     c.init_stores(ppw);
-    MacPlan m;
-    m.init(p.lay);
-    const int32_t s0 = m.nc0, s1 = m.nc0 + m.ns0 + m.nc1, s2 = s1 + m.ns1 + m.nc2;  // first scale row of each section
     uint32_t* flags = lds + kLdsFlags;
+    // a slot is reused only once stored: never let the producers sharing
+    // this SIMD starve the storer
+    __builtin_amdgcn_s_setprio(2);
     __builtin_amdgcn_s_waitcnt(0);
+    int32_t r = 0, g0 = 0;      // payload row; quantized units before the section
+    int32_t made = 0, pub = 0;  // scale rows made / published as stored
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= p.lay.n_sec) continue;
+        const int32_t kind = ZTCP_SEC_FIELD(p.lay, si, kind);
+        const int32_t nu = ZTCP_SEC_FIELD(p.lay, si, n_units);
+        const int32_t nblk = code_rows_per_unit(kind);  // 4, 8 or 16
+        const uint32_t sblk = ZTCP_SEC_FIELD(p.lay, si, s_off) / 64u;
+        const bool quant = kind != kSecRaw;
+        const int32_t ncode = nu * nblk;
 #pragma unroll 1
-    for (int32_t r = 0; r < m.total; ++r) {
-        const bool scale = (r >= s0 && r < s0 + m.ns0) || (r >= s1 && r < s1 + m.ns1) || (r >= s2 && r < s2 + m.ns2);
-        if (!scale) {
-            wait_ge<kDiagEgressWait>(&flags[kFlagRing + r % kRing], r + 1, c.wt);
+        for (int32_t cr = 0; cr < ncode; ++cr, ++r) {
+            const uint32_t* f = &flags[kFlagRing + r % kRing];
+            if (pub < made &&
+                (int32_t)__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < r + 1) {
+                publish_scales(flags, pub, made);
+                pub = made;
+            }
+            wait_ge<kDiagEgressWait>(f, r + 1, c.wt);
             store_row(lds + (r % kRing) * kRowWords, c, (uint32_t)kHeader + 64u * (uint32_t)r);
+            publish(&flags[kFlagStored], (uint32_t)r + 1u);  // the release orders the slot reads before it
+            if (quant && (cr & (nblk - 1)) == nblk - 1) {
+                const int32_t u = cr / nblk;
+                scale_row(c, g0 + u, sblk + (uint32_t)u);
+                if (++made - pub >= 4) {
+                    publish_scales(flags, pub, made);
+                    pub = made;
+                }
+            }
         }
-        publish(&flags[kFlagStored], (uint32_t)r + 1u);  // the release orders the slot reads before it
+        if (quant) {  // the section's scale rows reach the ring through the feeder
+#pragma unroll 1
+            for (int32_t i = 0; i < nu; ++i, ++r) publish(&flags[kFlagStored], (uint32_t)r + 1u);
+            g0 += nu;
+        }
     }
+    publish_scales(flags, pub, made);
 }
 
+// FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also the
+// extension kinds (e4m3, int4 per 32, asym8).  Separate instantiations keep
+// the extension's registers out of the reference kinds' kernel.
 template <int DT, int FAM>
 __global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];

@@ -558,10 +558,14 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
 template <int DT, int FAM>
 __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& lay) {
     uint32_t* flags = c.lds + kLdsFlags;
+    // (also reads how many rows the verify wave has absorbed, for the priority)
+    int32_t used = 0;
     auto grab = [&]() -> int32_t {
         uint32_t t = 0;
+        const uint32_t u = __hip_atomic_load(&flags[kFlagMacUsed], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (c.lane == 0)
             t = __hip_atomic_fetch_add(&flags[kFlagTask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        used = (int32_t)__builtin_amdgcn_readfirstlane(u);
         return (int32_t)__builtin_amdgcn_readfirstlane(t);
     };
     const int32_t total = total_tasks(lay);
@@ -577,6 +581,8 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
+        // a scale row is as urgent as the first code row of its unit
+        set_row_priority((k.scale ? (int32_t)(k.s.q_off / 64u) + k.u * k.s.nblk : k.mrow) - used);
         const Task nxt = task_info<FAM>(lay, tn);
         if (k.scale)
             scale_task(c, k, ct, nxt);

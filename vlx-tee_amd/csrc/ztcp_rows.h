@@ -85,8 +85,31 @@ __device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, cons
     }
 }
 
+// Marks 16 words as produced here: the computation of w[] stays before the
+// code that follows (an empty asm that reads and rewrites them), which keeps
+// the compiler from sinking it below a wait loop.
+__device__ __forceinline__ void pin_words(uint32_t (&w)[16]) {
+    asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]),
+                      "+v"(w[7]), "+v"(w[8]), "+v"(w[9]), "+v"(w[10]), "+v"(w[11]), "+v"(w[12]), "+v"(w[13]),
+                      "+v"(w[14]), "+v"(w[15]));
+}
+
 __device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
     __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// A SIMD issues the oldest of its ready waves first, so four worker waves of
+// equal priority progress at very different speeds (the youngest one's first
+// row finishes about four times later than the oldest one's).  Rows are
+// handed out in order while the MAC wave consumes them in order, so a row
+// held by a starved wave stalls the chain.  A worker therefore raises its
+// priority by how soon the MAC wave absorbs the row it is making: `lead` =
+// payload row - rows absorbed (wave-uniform).
+__device__ __forceinline__ void set_row_priority(int32_t lead) {
+    if (lead <= 4) __builtin_amdgcn_s_setprio(3);
+    else if (lead <= 10) __builtin_amdgcn_s_setprio(2);
+    else if (lead <= 18) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
 }
 
 // ---------------------------------------------------------------------------
