@@ -66,7 +66,9 @@ constexpr int kNumFlags = (kFlagExpired + 2) & ~1;   // even: the pointer table 
 constexpr int kLdsPtrs = kLdsFlags + kNumFlags;      // [2][64] output pointers (K, V)
 constexpr int kLdsLayouts = kLdsPtrs + 2 * 2 * 64;   // [kNumLayouts] Layout, one per header flags value
 constexpr int kLayoutWords = (int)(sizeof(Layout) / 4);
-constexpr int kLdsWords = kLdsLayouts + kNumLayouts * kLayoutWords;
+constexpr int kLdsHeaders = (kLdsLayouts + kNumLayouts * kLayoutWords + 3) & ~3;  // [64] 32-byte headers
+constexpr int kLdsWords = kLdsHeaders + 64 * 8;
+static_assert(kLdsHeaders % 4 == 0, "header table must be 16-byte aligned");
 static_assert(sizeof(Layout) % 4 == 0, "Layout is copied word by word");
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
 static_assert(kLdsPtrs % 2 == 0, "pointer table must be 8-byte aligned");
@@ -668,10 +670,10 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
 // Verdict of one page (cpp:2313-2355).  The payload's full 64-byte rows
 // come from the ring; its last (payload % 64) bytes and the tag are loaded
 // with the header.
-__device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t page, uint32_t* lds, int lane) {
+__device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t page, uint32_t* lds, int lane,
+                                               const uint4 h0, const uint4 h1) {
     const uint8_t* blob = ingress_blob(p, page);
     const uint8_t* pay = blob + kHeader;
-    const uint4 h0 = ldg16(blob, 0), h1 = ldg16(blob, 1);
     const int32_t total = (int32_t)(p.payload / 64u);
     const uint32_t tail0 = (uint32_t)total * 64u;
     const int ntail = (int)((p.payload - tail0) / 16u);  // 0..3 chunks of 16 bytes
@@ -714,13 +716,13 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool active = lane < ppw;
     const int64_t page = page0 + (active ? lane : 0);
-    // every wave derives the workgroup layout from the 64 headers itself
     const uint8_t* blob = ingress_blob(p, page);
-    const uint4 h0 = ldg16(blob, 0), h1 = ldg16(blob, 1);
-    const int li = layout_index(p, h0.x);
-    const uint64_t any_valid = __ballot(active && li >= 0);
-    const int li_wg = any_valid ? __builtin_amdgcn_readlane(li, (int)__builtin_ctzll(any_valid)) : -1;
-    const bool has_lay = li_wg >= 0;
+    // the 64 headers are loaded once, into LDS, for every wave
+    uint4* hdrs = reinterpret_cast<uint4*>(lds + kLdsHeaders);
+    if (threadIdx.x < 64) {
+        hdrs[2 * threadIdx.x] = ldg16(blob, 0);
+        hdrs[2 * threadIdx.x + 1] = ldg16(blob, 1);
+    }
     // the 24 layouts live in LDS: a table in registers or in the kernel
     // arguments would be copied to scratch memory once indexed by a variable
     Layout* layouts = reinterpret_cast<Layout*>(lds + kLdsLayouts);
@@ -738,10 +740,16 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         ptrs[64 + threadIdx.x] = reinterpret_cast<uint64_t>(v ? v : k);
     }
     __syncthreads();
+    // every wave derives the workgroup layout from the 64 headers itself
+    const uint4 h0 = hdrs[2 * lane], h1 = hdrs[2 * lane + 1];
+    const int li = layout_index(p, h0.x);
+    const uint64_t any_valid = __ballot(active && li >= 0);
+    const int li_wg = any_valid ? __builtin_amdgcn_readlane(li, (int)__builtin_ctzll(any_valid)) : -1;
+    const bool has_lay = li_wg >= 0;
     const Layout& lay = layouts[has_lay ? li_wg : 0];
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
-        flags[kFlagStatus + lane] = (uint32_t)verify_page(p, page, lds, lane);
+        flags[kFlagStatus + lane] = (uint32_t)verify_page(p, page, lds, lane, h0, h1);
     } else if (wave == 4) {
         ingress_feed(p, lds, lay, has_lay, blob + kHeader, lane);
     } else if ((wave & 3) != 0 && has_lay) {  // waves 8 and 12 share SIMD 0 and idle
