@@ -50,13 +50,14 @@ namespace ztcp {
 
 namespace {
 
-// 16 waves, four per SIMD: the MAC wave (0) and the scale-row feeder (4) on
-// SIMD 0 (waves 8 and 12 exit at once: producers there slow the MAC chain
-// down more than they add), the storer (1) and eleven producers on the other
-// three SIMDs.
-// 128 VGPRs each.
-constexpr int kEgressWaves = 16;
-constexpr int kEgressThreads = 64 * kEgressWaves;
+// 16 waves, four per SIMD, 128 VGPRs each: the MAC wave (0) and the
+// scale-row feeder (4) on SIMD 0 (waves 8 and 12 exit at once: producers
+// there slow the MAC chain down more than they add), the storer (1) and
+// eleven producers on the other three SIMDs.  The kernels of the extension
+// kinds run 12 waves, three per SIMD (eight producers): their quantizers need
+// more than 128 VGPRs, and 168 keep them out of scratch memory.
+template <int FAM>
+constexpr int egress_waves() { return FAM == 0 ? 16 : 12; }
 constexpr int kRing = 30;             // payload rows between their makers and the MAC wave
 constexpr int kStage = 8;             // units whose scales are staged at once
 constexpr int kLdsStage = kRing * kRowWords;
@@ -265,7 +266,7 @@ __device__ __forceinline__ void publish_scales(uint32_t* flags, int32_t from, in
 // 32): those rows load their chunks in two halves of four.
 template <int FAM>
 __device__ __forceinline__ bool two_halves(int32_t kind) {
-    return kind == kSecInt4 || (FAM == 1 && kind == kSecInt4G32);
+    return kind == kSecInt4 || (FAM >= 1 && kind == kSecInt4G32);
 }
 
 // Quantizes a row's first four chunks (w) into pt[] and its parameter words
@@ -283,10 +284,10 @@ __device__ __forceinline__ void quant_first(int32_t kind, const uint32_t (&w)[4]
             pt[t] = w[0][t];
             pt[8 + t] = w[1][t];
         }
-    } else if constexpr (FAM == 1) {
+    } else if constexpr (FAM >= 1) {
         if (kind == kSecE4m3) quant_half_e4m3<DT>(w, pt, sc);
-        else if (kind == kSecInt4G32) sc[0] = quant_half_int4g32<DT>(w, pt);
-        else sc[0] = quant_group64_asym8<DT>(w, pt);
+        else if (FAM == 1 || kind == kSecInt4G32) sc[0] = quant_half_int4g32<DT>(w, pt);
+        else if constexpr (FAM == 2) sc[0] = quant_group64_asym8<DT>(w, pt);
     }
 }
 
@@ -319,21 +320,42 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     ChaChaState st;
     st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
     st.double_rounds<4>();
-    if (kind == kSecInt4) quant_half<DT, 4>(w, pt + 8, sc + 2);
-    else if (FAM == 1 && kind == kSecInt4G32) sc[1] = quant_half_int4g32<DT>(w, pt + 8);
+    // the second half's scale words go to variables of their own: stores
+    // into sc at other indices than the first half's let the compiler merge
+    // the two quantizer calls into one store at a runtime index, which puts
+    // sc in scratch memory
+    uint32_t s2 = 0u, s3 = 0u;
+    if (kind == kSecInt4) {
+        uint32_t t[2];
+        quant_half<DT, 4>(w, pt + 8, t);
+        s2 = t[0];
+        s3 = t[1];
+    } else if (FAM >= 1 && kind == kSecInt4G32) {
+        s2 = quant_half_int4g32<DT>(w, pt + 8);
+    }
     if (nxt.valid) load_half(p, c.pg, nxt, 0, w);
     st.double_rounds<5>();
     if (kind != kSecRaw) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
         uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
         wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, c.wt);
-        const int sw = param_words_per_row(kind);  // parameter words of this row: 2, 4 or 1
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            if (t < sw) {
-                const int wd = row.j * sw + t;  // logical scale word of this lane's page
-                stage[quad_word(c.lane, wd >> 2) + (wd & 3)] = sc[t];
-            }
+        // parameter words of this row: 2 (int8, e4m3, int4 per 32), 4 (int4)
+        // or 1 (asym8), at logical words j * sw .. of this lane's page.  One
+        // branch per count: a loop bounded by a runtime count would index sc
+        // at run time and put it in scratch memory.
+        const int sw = param_words_per_row(kind);
+        if (sw == 4) {  // int4: two words per half
+            stage[quad_word(c.lane, row.j) + 0] = sc[0];
+            stage[quad_word(c.lane, row.j) + 1] = sc[1];
+            stage[quad_word(c.lane, row.j) + 2] = s2;
+            stage[quad_word(c.lane, row.j) + 3] = s3;
+        } else if (sw == 2) {  // int8, e4m3: both words from the first half; int4 per 32: one per half
+            const int wd = row.j * 2;
+            const bool split = FAM >= 1 && kind == kSecInt4G32;
+            stage[quad_word(c.lane, wd >> 2) + (wd & 3)] = sc[0];
+            stage[quad_word(c.lane, wd >> 2) + (wd & 3) + 1] = split ? s2 : sc[1];
+        } else {
+            stage[quad_word(c.lane, row.j >> 2) + (row.j & 3)] = sc[0];
         }
     }
     uint32_t ks[16];
@@ -607,10 +629,11 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
 }
 
 // FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also the
-// extension kinds (e4m3, int4 per 32, asym8).  Separate instantiations keep
-// the extension's registers out of the reference kinds' kernel.
+// extension kinds e4m3 and int4 per 32; FAM 2: also asym8, whose 64-element
+// groups need the most registers.  Separate instantiations keep each kind's
+// registers out of the kernels of layouts that do not use it.
 template <int DT, int FAM>
-__global__ __launch_bounds__(kEgressThreads) void egress_fused_kernel(EgressParams p) {
+__global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(EgressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
@@ -654,14 +677,20 @@ size_t egress_fused_lds_bytes() { return (size_t)kLdsWords * sizeof(uint32_t); }
 hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) {
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     const size_t lds = egress_fused_lds_bytes();  // above 64 KiB: gfx950 has 160 KiB per CU
-    bool ext = false;
-    for (int si = 0; si < p.lay.n_sec; ++si) ext = ext || is_extension_kind(p.lay.sec[si].kind);
-    const dim3 g((uint32_t)grid), b(kEgressThreads);
+    int fam = 0;  // the kind family of the layout (egress_fused_kernel)
+    for (int si = 0; si < p.lay.n_sec; ++si) {
+        const int32_t kind = p.lay.sec[si].kind;
+        if (kind == kSecAsym8) fam = 2;
+        else if (is_extension_kind(kind) && fam < 1) fam = 1;
+    }
+    const dim3 g((uint32_t)grid), b((uint32_t)(64 * (fam == 0 ? egress_waves<0>() : egress_waves<1>())));
     if (dtype == kHotBf16) {
-        if (ext) hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 1>), g, b, lds, s, p);
+        if (fam == 2) hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 2>), g, b, lds, s, p);
+        else if (fam == 1) hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 1>), g, b, lds, s, p);
         else hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 0>), g, b, lds, s, p);
     } else {
-        if (ext) hipLaunchKernelGGL((egress_fused_kernel<kHotFp16, 1>), g, b, lds, s, p);
+        if (fam == 2) hipLaunchKernelGGL((egress_fused_kernel<kHotFp16, 2>), g, b, lds, s, p);
+        else if (fam == 1) hipLaunchKernelGGL((egress_fused_kernel<kHotFp16, 1>), g, b, lds, s, p);
         else hipLaunchKernelGGL((egress_fused_kernel<kHotFp16, 0>), g, b, lds, s, p);
     }
     return hipGetLastError();
