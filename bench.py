@@ -269,6 +269,31 @@ def _rounded(d: dict) -> dict:
             for k, v in d.items()}
 
 
+def _describe(wname: str) -> str:
+    """One line naming the workload's page shape, kinds and input distribution."""
+    _package()
+    from vlx_tee_amd.spec import QuantPreset, RoPEMode
+    from vlx_tee_amd.workloads import WORKLOADS
+    w = WORKLOADS[wname]
+    if w.mla:
+        shape = (f"{w.n_pages} MLA pages of {w.num_tokens} tok x {w.head_dim} "
+                 f"({w.rope_dim} RoPE + {w.head_dim - w.rope_dim} latent), BF16")
+        dist = f"latent N(0,{w.sigma:g}), RoPE N(0,{w.rope_sigma:g})"
+    else:
+        shape = (f"{w.n_pages} pages of {w.num_tokens} tok x {w.num_heads} KV heads x head_dim "
+                 f"{w.head_dim}, K+V BF16")
+        dist = f"N(0,{w.sigma:g}) with RoPE dims x{w.rope_scale:g}"
+    if w.outlier_frac:
+        dist += f", {w.outlier_frac:.0%} of channels x{w.outlier_scale:g}"
+    hot = w.n_pages * w.hot_bytes_per_page
+    layers = w.n_pages // w.pages_per_layer
+    out = (f"{wname}: {w.pages_per_layer * w.num_tokens} tok x {layers} layers = {shape} ({hot / 2**30:.3g} GiB hot), {QuantPreset(w.preset).name} + "
+           f"{RoPEMode(w.rope_mode).name}, {dist}")
+    if w.tamper_frac:
+        out += f", ingress over a copy with one bit flipped in {w.tamper_frac:.0%} of the pages"
+    return out + ", one descriptor-batch launch per direction"
+
+
 def _traffic(kernel: str, workload: str):
     """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
     f = REPO / "profiles" / "hbm_traffic.json"
@@ -328,9 +353,7 @@ def main() -> None:
         "dtype": "u32",
         "data": "synthetic",
         "config": {
-            "workload": (f"{a.workload}: 4096 tok x 64 layers = {r['pages']} pages of 16 tok x 8 KV "
-                         "heads x head_dim 128, K+V BF16 (1 GiB hot), K8V4_ASYM + PRESERVE_FP8, "
-                         "N(0,1) with RoPE dims x8, one descriptor-batch launch per direction"),
+            "workload": _describe(a.workload),
             "pages": r["pages"], "hot_bytes": r["hot_bytes"], "wire_bytes": r["wire_bytes"],
         },
         "roofline": {
