@@ -462,14 +462,36 @@ __device__ __forceinline__ GroupCodes quant_group_exact(uint32_t w0, uint32_t w1
     return r;
 }
 
-// fp16(amax / C) for the fast path (see above); valid when the result is normal.
-template <int BITS>
-__device__ __forceinline__ uint32_t scale_fast(float amax) {
-    constexpr float C = BITS == 8 ? 127.0f : 7.0f;
-    constexpr float rC = BITS == 8 ? (1.0f / 127.0f) : (1.0f / 7.0f);
+// amax / C in fp32 for the fast paths: a corrected quotient (see above), one
+// fp32 rounding.
+template <int CI>
+__device__ __forceinline__ float quotient_fast(float amax) {
+    constexpr float C = (float)CI;
+    constexpr float rC = 1.0f / (float)CI;
     const float q0 = amax * rC;
     const float r = __builtin_fmaf(-q0, C, amax);
-    return f32_to_f16(__builtin_fmaf(r, rC, q0));
+    return __builtin_fmaf(r, rC, q0);
+}
+
+// The int8 / int4 scale fp16(amax / C), C = 127 / 7; valid when the result is
+// normal.  The compiler folds the last fma and the fp16 conversion into one
+// mixed-precision instruction, which rounds once from the exact value where
+// the reference rounds to fp32 first; ztcp_selftest shows the two agree for
+// every amax of both hot dtypes whenever the result is a normal fp16 value
+// (the quantizers send every other scale to their exact path).
+template <int BITS>
+__device__ __forceinline__ uint32_t scale_fast(float amax) {
+    return f32_to_f16(quotient_fast<BITS == 8 ? 127 : 7>(amax));
+}
+
+// The e4m3 scale fp16(amax / 448) for every amax >= 1e-6: the quotient equals
+// the IEEE one for every amax of both hot dtypes, and the empty asm keeps its
+// fp32 rounding, so fp16 subnormal results round as the reference's do
+// (ztcp_selftest checks every amax).
+__device__ __forceinline__ uint32_t scale_e4m3(float amax) {
+    float q = quotient_fast<448>(amax);
+    asm volatile("" : "+v"(q));
+    return f32_to_f16(q);
 }
 
 // 1 / s for a positive finite fp16 value s: Newton-refined v_rcp_f32.
@@ -486,18 +508,23 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint3
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
-// One group: code words (4 for int8, 2 for int4, the rest zero) and the fp16
-// scale bits, returned by value from both paths so that the caller's
-// registers never go through memory.
-template <int DT, int BITS>
-__device__ __forceinline__ GroupCodes quant_group_codes(const uint32_t w[8]) {
-    float f[16];
+// The 16 elements of a group as fp32 (element 2i from the low half of word i).
+template <int DT>
+__device__ __forceinline__ void hot_floats(const uint32_t w[8], float f[16]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         f[2 * i] = hot_lo<DT>(w[i]);
         f[2 * i + 1] = hot_hi<DT>(w[i]);
     }
-    // amax (NaN-free groups: max3 over |f| equals the reference's compare loop)
+}
+
+// max(1e-6, max |f|) by v_max3.  It equals the reference's compare loop
+// whenever the result is finite: a NaN element is either skipped, as the
+// compare loop skips it, or makes the result NaN, which sends the group to
+// the caller's exact path.  (The int8 and int4 fast paths then still write
+// the reference's code 0 for a skipped NaN element: the low bits of a NaN
+// sum are zero.)
+__device__ __forceinline__ float amax16(const float f[16]) {
     float m0 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[0]), fabsf(f[1])), fabsf(f[2]));
     float m1 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[3]), fabsf(f[4])), fabsf(f[5]));
     float m2 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[6]), fabsf(f[7])), fabsf(f[8]));
@@ -505,7 +532,30 @@ __device__ __forceinline__ GroupCodes quant_group_codes(const uint32_t w[8]) {
     float m4 = __builtin_fmaxf(__builtin_fmaxf(fabsf(f[12]), fabsf(f[13])), fabsf(f[14]));
     m0 = __builtin_fmaxf(__builtin_fmaxf(m0, m1), m2);
     m3 = __builtin_fmaxf(__builtin_fmaxf(m3, m4), fabsf(f[15]));
-    const float amax = __builtin_fmaxf(__builtin_fmaxf(m0, m3), 1e-6f);
+    return __builtin_fmaxf(__builtin_fmaxf(m0, m3), 1e-6f);
+}
+
+// int4 codes of 16 elements with a normal scale: with |v * inv| <= 7 * (1 +
+// 2^-10) < 7.5 no clamp is needed, and adding 1.5 * 2^23 + 8 rounds to
+// nearest even in that fp32 add; bits 0..3 of each sum hold q + 8 and bits
+// 4..7 are zero.  Element 2i goes to the low nibble of byte i.
+__device__ __forceinline__ void int4_codes_fast(const float f[16], float inv, uint32_t& q0, uint32_t& q1) {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        b[i] = (__float_as_uint(f[2 * i + 1] * inv + 12582920.0f) << 4) | __float_as_uint(f[2 * i] * inv + 12582920.0f);
+    q0 = pack_low_bytes(b[0], b[1], b[2], b[3]);
+    q1 = pack_low_bytes(b[4], b[5], b[6], b[7]);
+}
+
+// One group: code words (4 for int8, 2 for int4, the rest zero) and the fp16
+// scale bits, returned by value from both paths so that the caller's
+// registers never go through memory.
+template <int DT, int BITS>
+__device__ __forceinline__ GroupCodes quant_group_codes(const uint32_t w[8]) {
+    float f[16];
+    hot_floats<DT>(w, f);
+    const float amax = amax16(f);
     const uint32_t sb = scale_fast<BITS>(amax);
     // exact path: NaN / inf elements (amax not < inf), scale zero / subnormal / inf
     const bool special = !(amax < __builtin_inff()) || (sb - 0x0400u) >= (0x7C00u - 0x0400u);
@@ -523,13 +573,7 @@ __device__ __forceinline__ GroupCodes quant_group_codes(const uint32_t w[8]) {
         r.q2 = pack_low_bytes(t[8], t[9], t[10], t[11]);
         r.q3 = pack_low_bytes(t[12], t[13], t[14], t[15]);
     } else {
-        uint32_t b[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)  // bits 0..3 of each sum hold q + 8; bits 4..7 are zero
-            b[i] = (__float_as_uint(f[2 * i + 1] * inv + 12582920.0f) << 4) |
-                   __float_as_uint(f[2 * i] * inv + 12582920.0f);
-        r.q0 = pack_low_bytes(b[0], b[1], b[2], b[3]);
-        r.q1 = pack_low_bytes(b[4], b[5], b[6], b[7]);
+        int4_codes_fast(f, inv, r.q0, r.q1);
         r.q2 = 0u;
         r.q3 = 0u;
     }
@@ -731,12 +775,69 @@ __device__ __forceinline__ void e4m3_codes(const uint32_t w[8], float inv, uint3
     }
 }
 
-// FP8 e4m3, 16-element group: s = fp16(amax / 448).  Returns the scale bits.
+// max |element| of a group as a 16-bit pattern: bf16 and fp16 magnitudes
+// order like their bit patterns, and every NaN pattern lies above +inf's.
+__device__ __forceinline__ uint32_t amax_bits16(const uint32_t w[8]) {
+    using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
+    u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
+    return m.x > m.y ? m.x : m.y;
+}
+
+// FP8 e4m3, 16-element group: s = fp16(amax / 448), IEEE division and
+// reciprocal, codes by the saturating conversion with NaN -> 0 (the oracle's
+// zo_quant_group16_e4m3).  Cold path for groups with NaN or infinite
+// elements and for zero or infinite scales.
+template <int DT>
+__device__ __forceinline__ GroupCodes e4m3_group_exact(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                     uint32_t w4, uint32_t w5, uint32_t w6, uint32_t w7) {
+    const uint32_t w[8] = {w0, w1, w2, w3, w4, w5, w6, w7};
+    GroupCodes r;
+    r.scale = f32_to_f16(group_amax16<DT>(w) / 448.0f);
+    uint32_t q[4];
+    e4m3_codes<DT>(w, 1.0f / f16_to_f32(r.scale), q);
+    r.q0 = q[0]; r.q1 = q[1]; r.q2 = q[2]; r.q3 = q[3];
+    return r;
+}
+
+// The same codes with finite elements and a finite nonzero scale: amax from
+// the 16-bit magnitudes, the scale by scale_e4m3, the reciprocal by recip_fast
+// (exact for every positive finite fp16 value); the products are finite, so
+// the clamp alone prepares them for the conversion.
+template <int DT>
+__device__ __forceinline__ GroupCodes e4m3_group_codes(const uint32_t w[8]) {
+    const uint32_t mb = amax_bits16(w);
+    const float m = DT == kHotBf16 ? __uint_as_float(mb << 16) : f16_to_f32(mb);
+    const uint32_t sb = scale_e4m3(__builtin_fmaxf(m, 1e-6f));
+    const bool special = mb >= (DT == kHotBf16 ? 0x7F80u : 0x7C00u) || sb == 0u || sb >= 0x7C00u;
+    if (__builtin_expect(special, 0))
+        return e4m3_group_exact<DT>(w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]);
+    const float inv = recip_fast(f16_to_f32(sb));
+    GroupCodes r;
+    r.scale = sb;
+    uint32_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e0 = w[2 * j], e1 = w[2 * j + 1];
+        const uint32_t lo =
+            e4m3_pair_hw(__builtin_amdgcn_fmed3f(mul_keep_sign<DT>(hot_lo<DT>(e0), inv), -448.0f, 448.0f),
+                         __builtin_amdgcn_fmed3f(mul_keep_sign<DT>(hot_hi<DT>(e0), inv), -448.0f, 448.0f));
+        const uint32_t hi =
+            e4m3_pair_hw(__builtin_amdgcn_fmed3f(mul_keep_sign<DT>(hot_lo<DT>(e1), inv), -448.0f, 448.0f),
+                         __builtin_amdgcn_fmed3f(mul_keep_sign<DT>(hot_hi<DT>(e1), inv), -448.0f, 448.0f));
+        q[j] = lo | (hi << 16);
+    }
+    r.q0 = q[0]; r.q1 = q[1]; r.q2 = q[2]; r.q3 = q[3];
+    return r;
+}
+
+// FP8 e4m3, 16-element group.  Returns the scale bits.
 template <int DT>
 __device__ __forceinline__ uint32_t quant_group_e4m3(const uint32_t w[8], uint32_t q[4]) {
-    const uint32_t sb = f32_to_f16(group_amax16<DT>(w) / 448.0f);
-    e4m3_codes<DT>(w, 1.0f / f16_to_f32(sb), q);
-    return sb;
+    const GroupCodes r = e4m3_group_codes<DT>(w);
+    q[0] = r.q0; q[1] = r.q1; q[2] = r.q2; q[3] = r.q3;
+    return r.scale;
 }
 
 // int4 codes of one 16-element chunk with inv (the reference's int4 formula,
@@ -764,14 +865,34 @@ __device__ __forceinline__ void int4_codes(const uint32_t w[8], float inv, uint3
     }
 }
 
-// int4 over a 32-element group (chunks a, b): s = fp16(max(amax_a, amax_b) / 7).
+// int4 over a 32-element group (chunks a, b): s = fp16(max(amax_a, amax_b) / 7),
+// IEEE division and reciprocal (the oracle's zo_quant_group32_int4).  Cold
+// path for groups with non-finite elements and for scales that are not
+// normal fp16 values.
 template <int DT>
-__device__ __forceinline__ uint32_t quant_group32_int4(const uint32_t a[8], const uint32_t b[8], uint32_t q[4]) {
+__device__ __forceinline__ uint32_t int4g32_exact(const uint32_t a[8], const uint32_t b[8], uint32_t q[4]) {
     const float ma = group_amax16<DT>(a), mb = group_amax16<DT>(b);
     const uint32_t sb = f32_to_f16((mb > ma ? mb : ma) / 7.0f);
     const float inv = 1.0f / f16_to_f32(sb);
     int4_codes<DT>(a, inv, q);
     int4_codes<DT>(b, inv, q + 2);
+    return sb;
+}
+
+// The same with the int4 fast path of profile S (scale_fast, recip_fast and
+// rounding by the 1.5 * 2^23 sum) whenever the scale is a normal fp16 value.
+template <int DT>
+__device__ __forceinline__ uint32_t quant_group32_int4(const uint32_t a[8], const uint32_t b[8], uint32_t q[4]) {
+    float fa[16], fb[16];
+    hot_floats<DT>(a, fa);
+    hot_floats<DT>(b, fb);
+    const float amax = __builtin_fmaxf(amax16(fa), amax16(fb));
+    const uint32_t sb = scale_fast<4>(amax);
+    const bool special = !(amax < __builtin_inff()) || (sb - 0x0400u) >= (0x7C00u - 0x0400u);
+    if (__builtin_expect(special, 0)) return int4g32_exact<DT>(a, b, q);
+    const float inv = recip_fast(f16_to_f32(sb));
+    int4_codes_fast(fa, inv, q[0], q[1]);
+    int4_codes_fast(fb, inv, q[2], q[3]);
     return sb;
 }
 

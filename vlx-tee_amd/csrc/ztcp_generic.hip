@@ -300,8 +300,10 @@ __global__ void siphash_kernel(const uint8_t* data, uint64_t len, uint64_t mk0, 
 // ---- self-test of the fast quantizer arithmetic -------------------------------
 // Thread i covers magnitude bits i of both hot dtypes (amax candidates) and,
 // for i < 0x7C00, the fp16 scale with bits i (reciprocal candidates).
-// Violations: a fast scale that is a normal fp16 value but differs from
-// fp16(amax / C) by IEEE division, or a fast reciprocal that differs from 1 / s.
+// Violations: an int8 / int4 fast scale that is a normal fp16 value but
+// differs from fp16(amax / C) by IEEE division, an e4m3 fast scale that
+// differs from fp16(amax / 448) at all, or a fast reciprocal that differs
+// from 1 / s.
 __global__ void selftest_kernel(unsigned int* bad) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= 0x8000u) return;
@@ -313,6 +315,7 @@ __global__ void selftest_kernel(unsigned int* bad) {
         const uint32_t f8 = scale_fast<8>(a), f4 = scale_fast<4>(a);
         if (f8 >= 0x0400u && f8 < 0x7C00u && f8 != f32_to_f16(a / 127.0f)) ++n;
         if (f4 >= 0x0400u && f4 < 0x7C00u && f4 != f32_to_f16(a / 7.0f)) ++n;
+        if (scale_e4m3(a) != f32_to_f16(a / 448.0f)) ++n;  // e4m3: every result
     }
     if (i > 0 && i < 0x7C00u) {
         const float sv = f16_to_f32(i);
