@@ -5,25 +5,24 @@
 // fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004).
 //
 // Work decomposition (one workgroup = up to 64 pages, 16 waves, four per
-// SIMD; lane = page in every wave):
+// SIMD, or 12 for the extension kinds; lane = page in every wave):
 //   * A "row" is one 64-byte keystream block position of the payload, for all
 //     pages of the workgroup.  Every payload block is exactly one row: a code
 //     row (4 int8 / e4m3 / int4-per-32 groups, 8 int4 groups, 2 raw groups
 //     or 1 asym8 group) or a scale row (the 64 parameter bytes of one unit).
-//   * Eleven producer waves (on SIMDs 1-3) take code rows in order from an
-//     LDS counter.  A code row quantizes its groups (loaded a row ahead),
-//     stages the scales in LDS, computes the keystream, XORs, and writes the
-//     ciphertext into a ring of row slots in LDS at its place in payload
-//     order.  The wave that stages a unit's last scales (an LDS counter per
-//     staging slot) also makes the unit's scale row during its next code
-//     row: it encrypts the staged scales and stores them to the blobs,
-//     transposed (four lanes per page, 64 contiguous bytes per page per
-//     store).
+//   * Eleven producer waves (on SIMDs 1-3; eight in the extension kinds'
+//     12-wave kernels) take code rows in order from an LDS counter.  A code
+//     row quantizes its groups (loaded a row ahead), stages the scales in
+//     LDS, computes the keystream, XORs, and writes the ciphertext into a
+//     ring of row slots in LDS at its place in payload order.
 //   * A storer wave (wave 1, SIMD 1) stores every code row from the ring to
-//     the blobs the same transposed way, in payload order.  Producers issue
-//     no code-row stores: a wave's wait for its own loads also waits for
-//     every store it issued before them, which exposed the int4 rows' second
-//     loads; and the MAC wave's SIMD is kept free of stores.
+//     the blobs, in payload order, transposed (four lanes per page, 64
+//     contiguous bytes per page per store).  After a unit's last code row
+//     it also makes the unit's scale row: it encrypts the staged scales,
+//     stores them the same way and frees the staging slot.  Producers issue
+//     no stores: a wave's wait for its own loads also waits for every store
+//     it issued before them, which exposed the int4 rows' second loads; and
+//     the MAC wave's SIMD is kept free of stores.
 //   * Wave 0 runs SipHash for one page per lane, at raised priority on SIMD
 //     0.  It absorbs the header, then the payload rows in order from the
 //     ring, so it never reads global memory.  Scale rows reach the ring
@@ -35,9 +34,9 @@
 //   * Hand-offs are monotonic LDS counters with workgroup-scope
 //     release/acquire: ring_flag[slot] = payload row index + 1 when written,
 //     mac_used = rows absorbed and stored = rows stored (a slot is free once
-//     both have passed it), stage_flag[slot] = unit + 1
-//     when a scale row has read its staging slot, scale_flag[slot] = unit + 1
-//     once the scale row's stores have completed.  Every wait is bounded; an
+//     both have passed it), stage_flag[slot] = unit + 1 when a scale row
+//     has read its staging slot, scale_flag[slot] = unit + 1 once the scale
+//     row's stores have completed.  Every wait is bounded; an
 //     expired wait sets a sticky diagnostic bit and the kernel still ends.
 //     Waits only point backwards in row order, so progress never depends on
 //     a later row.
