@@ -148,7 +148,7 @@ template <uint32_t DIAG, class OnQuad>
 __device__ __forceinline__ void mac_absorb(const Waiter& wt, const uint32_t* ring, const uint32_t* ring_flags,
                                            uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want,
                                            bool ready, OnQuad& on_quad, const MacRow& prev, bool has_prev) {
-    if (!ready) {
+    if (__builtin_expect(!ready, 0)) {
         wait_ge<DIAG>(ring_flags + r.slot, want, wt);
 #pragma unroll
         for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
