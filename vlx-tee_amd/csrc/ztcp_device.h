@@ -879,20 +879,34 @@ __device__ __forceinline__ uint32_t int4g32_exact(const uint32_t a[8], const uin
     return sb;
 }
 
+// int4 codes of 16 elements (words w) with a normal scale, each element
+// converted where it is used: the int4_codes_fast sums without a float array.
+template <int DT>
+__device__ __forceinline__ void int4_codes_fast_w(const uint32_t w[8], float inv, uint32_t& q0, uint32_t& q1) {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        b[i] = (__float_as_uint(hot_hi<DT>(w[i]) * inv + 12582920.0f) << 4) |
+               __float_as_uint(hot_lo<DT>(w[i]) * inv + 12582920.0f);
+    q0 = pack_low_bytes(b[0], b[1], b[2], b[3]);
+    q1 = pack_low_bytes(b[4], b[5], b[6], b[7]);
+}
+
 // The same with the int4 fast path of profile S (scale_fast, recip_fast and
-// rounding by the 1.5 * 2^23 sum) whenever the scale is a normal fp16 value.
+// rounding by the 1.5 * 2^23 sum) whenever the elements are finite and the
+// scale is a normal fp16 value.  amax comes from the 16-bit magnitudes of
+// both chunks (amax_bits16), so no chunk is held as fp32 values.
 template <int DT>
 __device__ __forceinline__ uint32_t quant_group32_int4(const uint32_t a[8], const uint32_t b[8], uint32_t q[4]) {
-    float fa[16], fb[16];
-    hot_floats<DT>(a, fa);
-    hot_floats<DT>(b, fb);
-    const float amax = __builtin_fmaxf(amax16(fa), amax16(fb));
-    const uint32_t sb = scale_fast<4>(amax);
-    const bool special = !(amax < __builtin_inff()) || (sb - 0x0400u) >= (0x7C00u - 0x0400u);
+    const uint32_t ma = amax_bits16(a), mbits = amax_bits16(b);
+    const uint32_t mb = ma > mbits ? ma : mbits;
+    const float m = DT == kHotBf16 ? __uint_as_float(mb << 16) : f16_to_f32(mb);
+    const uint32_t sb = scale_fast<4>(__builtin_fmaxf(m, 1e-6f));
+    const bool special = mb >= (DT == kHotBf16 ? 0x7F80u : 0x7C00u) || (sb - 0x0400u) >= (0x7C00u - 0x0400u);
     if (__builtin_expect(special, 0)) return int4g32_exact<DT>(a, b, q);
     const float inv = recip_fast(f16_to_f32(sb));
-    int4_codes_fast(fa, inv, q[0], q[1]);
-    int4_codes_fast(fb, inv, q[2], q[3]);
+    int4_codes_fast_w<DT>(a, inv, q[0], q[1]);
+    int4_codes_fast_w<DT>(b, inv, q[2], q[3]);
     return sb;
 }
 

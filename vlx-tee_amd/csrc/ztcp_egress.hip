@@ -5,13 +5,14 @@
 // fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004).
 //
 // Work decomposition (one workgroup = up to 64 pages, 16 waves, four per
-// SIMD, or 12 for the extension kinds; lane = page in every wave):
+// SIMD, or 12 for the int4-per-32 and asym8 kinds; lane = page in every
+// wave):
 //   * A "row" is one 64-byte keystream block position of the payload, for all
 //     pages of the workgroup.  Every payload block is exactly one row: a code
 //     row (4 int8 / e4m3 / int4-per-32 groups, 8 int4 groups, 2 raw groups
 //     or 1 asym8 group) or a scale row (the 64 parameter bytes of one unit).
-//   * Eleven producer waves (on SIMDs 1-3; eight in the extension kinds'
-//     12-wave kernels) take code rows in order from an LDS counter.  A code
+//   * Eleven producer waves (on SIMDs 1-3; eight in the 12-wave kernels)
+//     take code rows in order from an LDS counter.  A code
 //     row quantizes its groups (loaded a row ahead), stages the scales in
 //     LDS, computes the keystream, XORs, and writes the ciphertext into a
 //     ring of row slots in LDS at its place in payload order.
@@ -52,11 +53,12 @@ namespace {
 // 16 waves, four per SIMD, 128 VGPRs each: the MAC wave (0) and the
 // scale-row feeder (4) on SIMD 0 (waves 8 and 12 exit at once: producers
 // there slow the MAC chain down more than they add), the storer (1) and
-// eleven producers on the other three SIMDs.  The kernels of the extension
-// kinds run 12 waves, three per SIMD (eight producers): their quantizers need
-// more than 128 VGPRs, and 168 keep them out of scratch memory.
+// eleven producers on the other three SIMDs.  The kernels of the int4-per-32
+// and asym8 kinds run 12 waves, three per SIMD (eight producers): their
+// quantizers need more than 128 VGPRs, and 168 keep them out of scratch
+// memory.
 template <int FAM>
-constexpr int egress_waves() { return FAM == 0 ? 16 : 12; }
+constexpr int egress_waves() { return FAM <= 1 ? 16 : 12; }  // family 2's quantizers need 168 VGPRs
 constexpr int kRing = 30;             // payload rows between their makers and the MAC wave
 constexpr int kStage = 8;             // units whose scales are staged at once
 constexpr int kLdsStage = kRing * kRowWords;
@@ -265,7 +267,7 @@ __device__ __forceinline__ void publish_scales(uint32_t* flags, int32_t from, in
 // 32): those rows load their chunks in two halves of four.
 template <int FAM>
 __device__ __forceinline__ bool two_halves(int32_t kind) {
-    return kind == kSecInt4 || (FAM >= 1 && kind == kSecInt4G32);
+    return kind == kSecInt4 || (FAM == 2 && kind == kSecInt4G32);
 }
 
 // Quantizes a row's first four chunks (w) into pt[] and its parameter words
@@ -284,9 +286,11 @@ __device__ __forceinline__ void quant_first(int32_t kind, const uint32_t (&w)[4]
             pt[8 + t] = w[1][t];
         }
     } else if constexpr (FAM >= 1) {
-        if (kind == kSecE4m3) quant_half_e4m3<DT>(w, pt, sc);
-        else if (FAM == 1 || kind == kSecInt4G32) sc[0] = quant_half_int4g32<DT>(w, pt);
-        else if constexpr (FAM == 2) sc[0] = quant_group64_asym8<DT>(w, pt);
+        if (FAM == 1 || kind == kSecE4m3) quant_half_e4m3<DT>(w, pt, sc);
+        else if constexpr (FAM == 2) {
+            if (kind == kSecInt4G32) sc[0] = quant_half_int4g32<DT>(w, pt);
+            else sc[0] = quant_group64_asym8<DT>(w, pt);
+        }
     }
 }
 
@@ -329,7 +333,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         quant_half<DT, 4>(w, pt + 8, t);
         s2 = t[0];
         s3 = t[1];
-    } else if (FAM >= 1 && kind == kSecInt4G32) {
+    } else if (FAM == 2 && kind == kSecInt4G32) {
         s2 = quant_half_int4g32<DT>(w, pt + 8);
     }
     if (nxt.valid) load_half(p, c.pg, nxt, 0, w);
@@ -350,7 +354,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
             stage[quad_word(c.lane, row.j) + 3] = s3;
         } else if (sw == 2) {  // int8, e4m3: both words from the first half; int4 per 32: one per half
             const int wd = row.j * 2;
-            const bool split = FAM >= 1 && kind == kSecInt4G32;
+            const bool split = FAM == 2 && kind == kSecInt4G32;
             stage[quad_word(c.lane, wd >> 2) + (wd & 3)] = sc[0];
             stage[quad_word(c.lane, wd >> 2) + (wd & 3) + 1] = split ? s2 : sc[1];
         } else {
@@ -627,10 +631,11 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
     publish_scales(flags, pub, made);
 }
 
-// FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also the
-// extension kinds e4m3 and int4 per 32; FAM 2: also asym8, whose 64-element
-// groups need the most registers.  Separate instantiations keep each kind's
-// registers out of the kernels of layouts that do not use it.
+// FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also e4m3
+// (16 waves, as FAM 0); FAM 2: also int4 per 32 and asym8, whose 32- and
+// 64-element groups need the most registers (12 waves, 168 VGPRs each).
+// Separate instantiations keep each kind's registers out of the kernels of
+// layouts that do not use it.
 template <int DT, int FAM>
 __global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(EgressParams p) {
     extern __shared__ __align__(16) uint32_t lds[];
@@ -679,10 +684,11 @@ hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) 
     int fam = 0;  // the kind family of the layout (egress_fused_kernel)
     for (int si = 0; si < p.lay.n_sec; ++si) {
         const int32_t kind = p.lay.sec[si].kind;
-        if (kind == kSecAsym8) fam = 2;
+        if (kind == kSecAsym8 || kind == kSecInt4G32) fam = 2;
         else if (is_extension_kind(kind) && fam < 1) fam = 1;
     }
-    const dim3 g((uint32_t)grid), b((uint32_t)(64 * (fam == 0 ? egress_waves<0>() : egress_waves<1>())));
+    const dim3 g((uint32_t)grid),
+        b((uint32_t)(64 * (fam == 0 ? egress_waves<0>() : (fam == 1 ? egress_waves<1>() : egress_waves<2>()))));
     if (dtype == kHotBf16) {
         if (fam == 2) hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 2>), g, b, lds, s, p);
         else if (fam == 1) hipLaunchKernelGGL((egress_fused_kernel<kHotBf16, 1>), g, b, lds, s, p);
