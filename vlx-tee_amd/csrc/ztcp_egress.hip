@@ -79,7 +79,6 @@ static_assert(kLdsBlobs % 2 == 0, "blob table must be 8-byte aligned");
 
 struct Row {
     int32_t valid;
-    int32_t scale;    // 1: last code row of its unit (quantized sections)
     int32_t u, j;     // unit in section, code block in unit
     int32_t g;        // unit index among the page's quantized units (staging slot order)
     int32_t cidx;     // code row index = production order
@@ -89,8 +88,8 @@ struct Row {
 };
 
 // Code row t: the payload's code blocks in order, which is also the order of
-// production.  A unit's scale row is produced right after its last code row,
-// by the same wave.
+// production.  (A unit's scale row is made by the storer wave once it has
+// stored the unit's last code row.)
 __device__ __forceinline__ Row row_info(const Layout& lay, int32_t t) {
     Row row{};
     int32_t cb = 0, qb = 0;
@@ -104,7 +103,6 @@ __device__ __forceinline__ Row row_info(const Layout& lay, int32_t t) {
             row.valid = 1;
             row.u = local / s.nblk;  // nblk is 8, 4 or 16
             row.j = local - row.u * s.nblk;
-            row.scale = s.kind != kSecRaw && row.j == s.nblk - 1;
             row.g = s.qunit_begin + row.u;
             row.cidx = t;
             row.mrow = t + qb;  // the scale rows of earlier sections come first
