@@ -647,17 +647,22 @@ __device__ __forceinline__ void dequant_group_int8(const uint32_t q[4], uint32_t
 template <int DT>
 __device__ __forceinline__ void dequant_group_int4(const uint32_t q[2], uint32_t scale_bits,
                                                    uint32_t out[8]) {
-    const float s = f16_to_f32(scale_bits & 0xFFFFu);
+    // Nibble n ^ 8 is n - 8 in 4-bit two's complement.  Moved to the high
+    // half of a byte it is the signed byte 16 (n - 8), which one sign-
+    // extending conversion per element turns into fp32 (as the int8 codes
+    // are); times s / 16 (exact: a power-of-two scaling of an fp16 value)
+    // that is exactly (n - 8) * s, with the same sign of zero, infinities
+    // and NaNs as the reference's (float)(n - 8) * s.
+    const float s16 = f16_to_f32(scale_bits & 0xFFFFu) * 0.0625f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        // nibble n ^ 8 is n - 8 in 4-bit two's complement: a signed field
-        // extract gives the code's value in one instruction
-        const int32_t x = (int32_t)(q[j] ^ 0x88888888u);
+        const uint32_t x = q[j] ^ 0x88888888u;
+        const int32_t hi = (int32_t)(x & 0xF0F0F0F0u);          // byte i: 16 x element 2i + 1
+        const int32_t lo = (int32_t)((x << 4) & 0xF0F0F0F0u);   // byte i: 16 x element 2i
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // (the builtin's result type is unsigned: the value is read as int32_t)
-            const float a = (float)(int32_t)__builtin_amdgcn_sbfe(x, 8u * i, 4u) * s;       // element 2i
-            const float b = (float)(int32_t)__builtin_amdgcn_sbfe(x, 8u * i + 4u, 4u) * s;  // element 2i + 1
+            const float a = (float)((lo << (24 - 8 * i)) >> 24) * s16;  // element 2i
+            const float b = (float)((hi << (24 - 8 * i)) >> 24) * s16;  // element 2i + 1
             out[4 * j + i] = pack_hot<DT>(a, b);
         }
     }
