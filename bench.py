@@ -15,6 +15,12 @@ pages resident in HBM and outputs preallocated: 4096 tokens x 64 layers =
               reference sources) on this host's cores, FP16 (its only dtype),
               on a bounded sample of the same pages
 
+Before the W warmup steps, each workload runs untimed egress + ingress pairs
+for --settle-seconds (0.3 s; half that for the extra workloads), so that the
+timed steps see the chip's clock under load rather than its climb from idle;
+the line reports the number of those pairs and the first pair's times from
+idle ("settle").
+
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload NAME]
 """
 from __future__ import annotations
@@ -50,7 +56,7 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def run_gpu(wname: str, steps: int, warmup: int) -> dict:
+def run_gpu(wname: str, steps: int, warmup: int, settle_s: float) -> dict:
     import numpy as np
     import torch
 
@@ -89,13 +95,46 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
                   per_page=bool(len(t_pages)), ext_layouts=w.extension, **geo, **keys)
 
     want_status = np.zeros(w.n_pages, dtype=np.int32)
+    egress()
+    torch.cuda.synchronize()
     if len(t_pages):
-        egress()
         blobs_in.copy_(blobs)
         idx = torch.from_numpy(t_pages).to(dev)
         cols = torch.from_numpy(t_bits // 8).to(dev)
         blobs_in[idx, cols] = blobs_in[idx, cols] ^ torch.from_numpy((1 << (t_bits % 8)).astype(np.uint8)).to(dev)
         want_status[t_pages] = -1  # any rejection verdict
+    # self-consistency: a second encode reproduces the blobs bit for bit
+    ref_blobs = blobs.clone()
+    egress()
+    torch.cuda.synchronize()
+    if not torch.equal(ref_blobs, blobs):
+        raise SystemExit("bench: egress is not deterministic")
+    del ref_blobs
+
+    # Settle: the chip leaves its idle clock over the first ~10 ms of load, and
+    # pairs timed from idle run about 10 % slower than under sustained load (a
+    # serving loop's state).  The same egress + ingress pairs run for at least
+    # `settle_s` before the warmup steps; the result reports how many, and the
+    # first pair's times from idle.
+    stream = torch.cuda.current_stream()
+    f0, f1, f2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    torch.cuda.synchronize()
+    ts = time.perf_counter()
+    f0.record(stream)
+    egress()
+    f1.record(stream)
+    ingress()
+    f2.record(stream)
+    settle_pairs = 1
+    while time.perf_counter() - ts < settle_s:
+        for _ in range(10):
+            egress()
+            ingress()
+        settle_pairs += 10
+        torch.cuda.synchronize()
+    settle = dict(pairs=settle_pairs, s=round(time.perf_counter() - ts, 3),
+                  first_pair_from_idle_ms=dict(egress=round(f0.elapsed_time(f1), 4),
+                                               ingress=round(f1.elapsed_time(f2), 4)))
     for _ in range(warmup):
         egress()
         ingress()
@@ -108,18 +147,10 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
             raise SystemExit(f"bench: {int(bad.sum())} pages with the wrong verdict {when}")
 
     check_status("after warmup")
-    # self-consistency: a second encode reproduces the blobs bit for bit
-    ref_blobs = blobs.clone()
-    egress()
-    torch.cuda.synchronize()
-    if not torch.equal(ref_blobs, blobs):
-        raise SystemExit("bench: egress is not deterministic")
-    del ref_blobs
     import vlx_tee_amd.native_hip_codec as H
 
     diag = H.device_diag()
 
-    stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
@@ -148,6 +179,7 @@ def run_gpu(wname: str, steps: int, warmup: int) -> dict:
         egress_hbm_frac=(hot + wire) / me / 1e6 / HBM_PEAK_GBPS,
         ingress_hbm_frac=(hot + wire) / mi / 1e6 / HBM_PEAK_GBPS,
         tampered_pages_rejected=f"{len(t_pages)}/{len(t_pages)}" if len(t_pages) else None,
+        settle=settle,
         device_diag=diag,
     )
     del k, v, blobs, blobs_in, ko, vo
@@ -315,6 +347,8 @@ def main() -> None:
                                        "c3_e4m3_tamper,c4_mla_int4g32"),
                     help="comma list of extra workloads")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--settle-seconds", type=float, default=0.3,
+                    help="untimed egress + ingress pairs before the warmup steps (clock leaves idle)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy kernel of BYTES (counter calibration)")
@@ -327,10 +361,10 @@ def main() -> None:
               "(pages shard independently); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
-    main_res = run_gpu(a.workload, a.steps, a.warmup)
+    main_res = run_gpu(a.workload, a.steps, a.warmup, a.settle_seconds)
     extras = {}
     for wn in [x for x in a.also.split(",") if x and x != a.workload]:
-        extras[wn] = run_gpu(wn, max(3, a.steps // 2), 2)
+        extras[wn] = run_gpu(wn, max(3, a.steps // 2), 2, a.settle_seconds / 2)
     cpu = None if a.no_cpu else cpu_baseline(a.workload, a.cpu_seconds)
 
     r = main_res
@@ -367,6 +401,7 @@ def main() -> None:
         "ingress": {k: round(r[k], 4) for k in ("ingress_ms", "ingress_hot_gbps", "ingress_wire_gbps", "ingress_hbm_frac")},
         "extra_workloads": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
                             for n, x in extras.items()},
+        "settle": r["settle"],
         "device_diag": r["device_diag"],
     }
     print(json.dumps(out))

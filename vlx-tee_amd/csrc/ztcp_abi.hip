@@ -56,8 +56,12 @@ int device_ctx(DeviceCtx** out) {
                   hipMalloc(&c->calls, sizeof(CallState) * kCallSlots) == hipSuccess &&
                   hipHostMalloc(&c->host_calls, sizeof(CallState) * kCallSlots, hipHostMallocDefault) == hipSuccess &&
                   hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+        // A slot's event only tells the host that the device is done with the
+        // slot's CallState, which only later device work touches: a device-scope
+        // release suffices, and spares each asynchronous call the system-scope
+        // fence (an L2 writeback and invalidate on every XCD).
         for (int i = 0; ok && i < kCallSlots; ++i)
-            ok = hipEventCreateWithFlags(&c->done[i], hipEventDisableTiming) == hipSuccess;
+            ok = hipEventCreateWithFlags(&c->done[i], hipEventDisableTiming | hipEventReleaseToDevice) == hipSuccess;
         if (!ok) return ZTCP_EHIP;  // the partial context is left unused (one per device, process lifetime)
         g_ctx[dev] = c;
     }
