@@ -187,6 +187,133 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float) -> dict:
     return res
 
 
+def run_small_egress(wname: str, steps: int) -> dict:
+    """Egress only of a small batch (the reference's peak-256 case,
+    research/benchmarks/bench_cold_page_pipeline.py:924-930): pages in HBM,
+    blobs into a preallocated buffer.  Timed twice: back to back, with the
+    8 MiB of hot pages resident in the caches ("warm"), and with the caches
+    flushed before every launch by writing a 1 GiB buffer ("flushed"); HIP
+    events bracket the egress launch alone."""
+    import torch
+
+    _package().load_native()
+    import vlx_tee_amd.pages as P
+    from vlx_tee_amd.workloads import MODEL_HASH, TENANT_HASH, WORKLOADS, generate, page_metadata, session_keys
+
+    w = WORKLOADS[wname]
+    dev = torch.device("cuda:0")
+    keys = session_keys()
+    k, v = generate(w, dev, torch.bfloat16)
+    th, seq, layers = page_metadata(w)
+    blobs = torch.empty((w.n_pages, w.blob_bytes), dtype=torch.uint8, device=dev)
+    d = P.build_descriptors(k, v, blobs, th, seq, layers)
+    geo = dict(num_tokens=w.num_tokens, num_heads=w.num_heads, head_dim=w.head_dim,
+               rope_dim=w.rope_dim, dtype=torch.bfloat16, is_mla_single_buffer=w.mla)
+
+    def egress():
+        P.egress(d, w.n_pages, preset=w.preset, rope_mode=w.rope_mode,
+                 expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
+                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, **geo, **keys)
+
+    egress()
+    torch.cuda.synchronize()
+    ref = blobs.clone()
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    warm, cold = [], []
+    for i in range(3 + steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        egress()
+        b.record(stream)
+        flush.fill_(i & 0xFF)
+        c, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c.record(stream)
+        egress()
+        e.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            warm.append(a.elapsed_time(b))
+            cold.append(c.elapsed_time(e))
+    if not torch.equal(ref, blobs):
+        raise SystemExit(f"bench: {wname} egress is not deterministic")
+    hot = w.n_pages * w.hot_bytes_per_page
+    wire = w.n_pages * w.blob_bytes
+    mw, mc = statistics.mean(warm), statistics.mean(cold)
+    res = dict(workload=wname, pages=w.n_pages, hot_bytes=hot, wire_bytes=wire, direction="egress only",
+               egress_ms_warm=mw, egress_ms_flushed=mc,
+               egress_hot_gbps_warm=hot / mw / 1e6, egress_wire_gbps_warm=wire / mw / 1e6,
+               egress_hot_gbps_flushed=hot / mc / 1e6, egress_wire_gbps_flushed=wire / mc / 1e6,
+               note=("one page per workgroup (256 of the 256 CUs): the launch lasts one page's "
+                     "SipHash chain, 1541 words in sequence"))
+    del k, v, blobs, flush, ref
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_wire_ring(wname: str, parts: int = 4, reps: int = 3) -> dict:
+    """The egress wire step (serving.WireRing): the prefix's blobs leave HBM
+    through two pinned host slots, one part of the pages per push.
+    "copy": the blobs are already encoded; the time from the first push to the
+    last landed copy.  "pipelined": egress of part i + 1 overlaps the copy of
+    part i on the ring's own stream; the time from the first egress launch to
+    the last landed copy.  Both are host wall clock over PCIe, so they are
+    reported beside, never as, the HBM-resident figures."""
+    import torch
+
+    _package().load_native()
+    import vlx_tee_amd.pages as P
+    import vlx_tee_amd.serving as SV
+    from vlx_tee_amd.workloads import MODEL_HASH, TENANT_HASH, WORKLOADS, generate, page_metadata, session_keys
+
+    w = WORKLOADS[wname]
+    dev = torch.device("cuda:0")
+    keys = session_keys()
+    k, v = generate(w, dev, torch.bfloat16)
+    th, seq, layers = page_metadata(w)
+    blobs = torch.empty((w.n_pages, w.blob_bytes), dtype=torch.uint8, device=dev)
+    d = P.build_descriptors(k, v, blobs, th, seq, layers)
+    geo = dict(num_tokens=w.num_tokens, num_heads=w.num_heads, head_dim=w.head_dim,
+               rope_dim=w.rope_dim, dtype=torch.bfloat16, is_mla_single_buffer=w.mla)
+    q = w.n_pages // parts
+
+    def egress(i):
+        P.egress(d[i * q:(i + 1) * q], q, preset=w.preset, rope_mode=w.rope_mode,
+                 expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
+                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, **geo, **keys)
+
+    ring = SV.WireRing(q * w.blob_bytes, n_slots=2)
+    copy_s, pipe_s = [], []
+    for rep in range(1 + reps):
+        for i in range(parts):
+            egress(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(parts):
+            ring.push(blobs[i * q:(i + 1) * q])
+        ring.wait((parts - 1) % 2)
+        ring.wait((parts - 2) % 2)
+        t1 = time.perf_counter()
+        for i in range(parts):
+            egress(i)
+            ring.push(blobs[i * q:(i + 1) * q])
+        ring.wait((parts - 1) % 2)
+        ring.wait((parts - 2) % 2)
+        t2 = time.perf_counter()
+        if rep:
+            copy_s.append(t1 - t0)
+            pipe_s.append(t2 - t1)
+    wire = w.n_pages * w.blob_bytes
+    mc, mp = statistics.mean(copy_s), statistics.mean(pipe_s)
+    res = dict(workload=wname, parts=parts, slot_bytes=q * w.blob_bytes, wire_bytes=wire,
+               copy_s=mc, pipelined_s=mp, copy_wire_gbps=wire / mc / 1e9,
+               pipelined_wire_gbps=wire / mp / 1e9, pipelined_hot_gbps=w.n_pages * w.hot_bytes_per_page / mp / 1e9,
+               note="device-to-host over PCIe into pinned slots, host wall clock; not an HBM figure")
+    del k, v, blobs, ring
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(wname: str, budget_s: float) -> dict | None:
     """The reference's C++ codec on this host (FP16), on a bounded page sample."""
     import numpy as np
@@ -346,10 +473,13 @@ def main() -> None:
     ap.add_argument("--also", default=("c2_int4_prefix1g,c3_fp8only_tamper,c4_mla_int4,c2_k8v4asym_prefix1g,"
                                        "c3_e4m3_tamper,c4_mla_int4g32"),
                     help="comma list of extra workloads")
+    ap.add_argument("--small", default="c1_int4_gqa256",
+                    help="comma list of small egress-only workloads (warm and cache-flushed)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--settle-seconds", type=float, default=0.3,
                     help="untimed egress + ingress pairs before the warmup steps (clock leaves idle)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-wire", action="store_true", help="skip the wire-ring (device-to-host) measurement")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy kernel of BYTES (counter calibration)")
     a = ap.parse_args()
@@ -365,6 +495,9 @@ def main() -> None:
     extras = {}
     for wn in [x for x in a.also.split(",") if x and x != a.workload]:
         extras[wn] = run_gpu(wn, max(3, a.steps // 2), 2, a.settle_seconds / 2)
+    for wn in [x for x in a.small.split(",") if x]:
+        extras[wn] = run_small_egress(wn, max(5, a.steps))
+    wire_ring = None if a.no_wire else run_wire_ring(a.workload)
     cpu = None if a.no_cpu else cpu_baseline(a.workload, a.cpu_seconds)
 
     r = main_res
@@ -401,6 +534,7 @@ def main() -> None:
         "ingress": {k: round(r[k], 4) for k in ("ingress_ms", "ingress_hot_gbps", "ingress_wire_gbps", "ingress_hbm_frac")},
         "extra_workloads": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in x.items()}
                             for n, x in extras.items()},
+        "wire_ring": None if wire_ring is None else _rounded(wire_ring),
         "settle": r["settle"],
         "device_diag": r["device_diag"],
     }
