@@ -257,6 +257,41 @@ int ztcp_device_diag(void);
  * fault.  Returns the previous value. */
 int64_t ztcp_debug_spin_limit(int64_t n);
 
+/* Serving-side steps around the codec (vlx-tee_amd/csrc/ztcp_serving.hip).
+ *
+ * Hit bitmap of per-page ingress verdicts: the PoisonShield per-page fallback
+ * (research/paper/main.tex:173), where a page that fails AAD, MAC or
+ * freshness checks is not written to hot memory and reads as a miss in the
+ * serving engine's hit bitmap, so the engine recomputes that prefix instead
+ * of failing the worker.  The reference describes the step but has no
+ * function for it.  page_status: DEVICE int32[n] as the per-page ingress
+ * writes it.  packed = 0: out is DEVICE uint8[n], 1 where the verdict is 0;
+ * packed = 1: out is DEVICE uint8[(n + 7) / 8], page i in bit i % 8 of byte
+ * i / 8 (least significant bit first), trailing bits 0.  Enqueued on stream. */
+int ztcp_hit_bitmap(const int32_t* page_status, int64_t n, uint8_t* out, int32_t packed, void* stream);
+
+/* Egress wire ring: a batch of blobs leaves HBM into the next of n_slots
+ * pinned host slots, on a copy stream of the ring's own that waits for the
+ * work already queued on the producer's stream (the egress launch that wrote
+ * the blobs), so the next batch's egress overlaps the copy.  The reference
+ * models this step only (research/benchmarks/bench_cold_page_pipeline.py:
+ * 1089-1162: blob bytes over a link after the codec).
+ *   create:  n_slots slots of slot_bytes on the current device.
+ *   push:    copies nbytes (<= slot_bytes) of DEVICE blobs into the next
+ *            slot, after the work queued on `stream`; *slot = its index.  A
+ *            slot is reused n_slots pushes later, after its previous copy
+ *            has landed, so the bytes wait returned stay valid until then.
+ *            Pushes from several host threads take slots in turn.
+ *   wait:    blocks until that slot's copy has landed; *host and *nbytes
+ *            give its bytes (HOST memory owned by the ring).
+ *   destroy: waits for the copies in flight, then frees the ring. */
+typedef struct ztcp_wire_ring ztcp_wire_ring;
+int ztcp_wire_ring_create(size_t slot_bytes, int32_t n_slots, ztcp_wire_ring** ring);
+int ztcp_wire_ring_push(ztcp_wire_ring* ring, const uint8_t* blobs, size_t nbytes, void* stream,
+                        int32_t* slot);
+int ztcp_wire_ring_wait(ztcp_wire_ring* ring, int32_t slot, const uint8_t** host, size_t* nbytes);
+int ztcp_wire_ring_destroy(ztcp_wire_ring* ring);
+
 /* Short description of a return code. */
 const char* ztcp_strerror(int code);
 

@@ -28,7 +28,8 @@ EXPORTS = (
     "ztcp_ingress_peak_into", "ztcp_ingress_peak_into_noalloc", "ztcp_ingress_batch",
     "ztcp_chacha20_xor", "ztcp_siphash128",
     "ztcp_selftest", "ztcp_device_diag", "ztcp_debug_spin_limit", "ztcp_strerror",
-    "ztcp_last_error",
+    "ztcp_last_error", "ztcp_hit_bitmap", "ztcp_wire_ring_create", "ztcp_wire_ring_push",
+    "ztcp_wire_ring_wait", "ztcp_wire_ring_destroy",
 )
 
 # Every symbol include/ztcp_keyring.h declares (host code, callable without a GPU).
@@ -114,6 +115,16 @@ def lib() -> C.CDLL:
     L.ztcp_strerror.restype = C.c_char_p
     L.ztcp_last_error.argtypes = []
     L.ztcp_last_error.restype = C.c_char_p
+    L.ztcp_hit_bitmap.argtypes = [P, i64, P, i32, P]
+    L.ztcp_hit_bitmap.restype = i32
+    L.ztcp_wire_ring_create.argtypes = [C.c_size_t, i32, C.POINTER(C.c_void_p)]
+    L.ztcp_wire_ring_create.restype = i32
+    L.ztcp_wire_ring_push.argtypes = [P, P, C.c_size_t, P, C.POINTER(C.c_int32)]
+    L.ztcp_wire_ring_push.restype = i32
+    L.ztcp_wire_ring_wait.argtypes = [P, i32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
+    L.ztcp_wire_ring_wait.restype = i32
+    L.ztcp_wire_ring_destroy.argtypes = [P]
+    L.ztcp_wire_ring_destroy.restype = i32
     _bind_keyring(L)
     _lib = L
     return L

@@ -12,41 +12,63 @@ WireRing: the egress wire step.  The reference only models it
   a 100GbE link after the codec).  Here a batch of blobs leaves HBM into a
   ring of pinned host slots on a copy stream of its own, ordered after the
   egress launch by an event, so the next batch's egress overlaps the copy.
+
+Both are the library's (include/ztcp.h: ztcp_hit_bitmap, ztcp_wire_ring_*);
+this module binds them to torch tensors.
 """
 from __future__ import annotations
 
+import ctypes as C
+
+import numpy as np
 import torch
 
+from . import _native as N
+
+
+def _stream(device: torch.device) -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _raise(rc: int, what: str) -> None:
+    if rc != N.OK:
+        raise RuntimeError(f"{what}: {N.strerror(rc)} (code {rc})")
 
 
 def hit_bitmap(page_status: torch.Tensor, packed: bool = False) -> torch.Tensor:
     """True for every page whose ingress verdict is 0 (verified and written).
 
-    ``page_status`` holds one int32 verdict per page, as the per-page ingress
-    writes it.  ``packed`` returns uint8 bytes instead, page i in bit i % 8
-    of byte i // 8 (least significant bit first), trailing bits 0."""
+    ``page_status`` is a 1-D int32 device tensor of per-page verdicts, as the
+    per-page ingress writes it; the bitmap is made on the device by the
+    library (ztcp_hit_bitmap) on the current stream.  ``packed`` returns
+    uint8 bytes instead, page i in bit i % 8 of byte i // 8 (least
+    significant bit first), trailing bits 0."""
     if page_status.dtype != torch.int32 or page_status.dim() != 1:
         raise ValueError("page_status must be a 1-D int32 tensor of per-page verdicts")
-    hits = page_status == 0
-    if not packed:
-        return hits
-    n = hits.numel()
-    pad = (-n) % 8
-    bits = torch.cat([hits, hits.new_zeros(pad)]).view(-1, 8).to(torch.uint8)
-    weights = torch.tensor([1, 2, 4, 8, 16, 32, 64, 128], dtype=torch.uint8, device=bits.device)
-    return (bits * weights).sum(dim=1, dtype=torch.uint8)
+    if not page_status.is_cuda:
+        raise ValueError("page_status must be a device tensor (the bitmap is made on the GPU)")
+    st = page_status.contiguous()
+    n = st.numel()
+    out = torch.empty((n + 7) // 8 if packed else n, dtype=torch.uint8 if packed else torch.bool,
+                      device=st.device)
+    with torch.cuda.device(st.device):
+        rc = N.lib().ztcp_hit_bitmap(C.c_void_p(st.data_ptr()), n, C.c_void_p(out.data_ptr()),
+                                     1 if packed else 0, _stream(st.device))
+    _raise(rc, "ztcp_hit_bitmap")
+    return out
 
 
 class WireRing:
-    """A ring of ``n_slots`` pinned host buffers of ``slot_bytes`` each.
+    """A ring of ``n_slots`` pinned host buffers of ``slot_bytes`` each, with a
+    copy stream of its own (the library's ztcp_wire_ring).
 
     ``push(blobs)`` copies a contiguous device tensor of blobs into the next
-    slot on the ring's own copy stream (default priority), after the work
-    already queued on the caller's current stream (the egress launch that
-    wrote the blobs), and returns the slot index.  ``wait(slot)`` blocks until
-    that copy has landed and returns the slot's bytes as a host tensor.  A
-    slot is reused after ``n_slots`` further pushes; its previous copy is
-    waited for first, so the bytes ``wait`` returned stay valid until then."""
+    slot after the work already queued on the caller's current stream (the
+    egress launch that wrote the blobs) and returns the slot index.
+    ``wait(slot)`` blocks until that copy has landed and returns the slot's
+    bytes as a host tensor (a view of the pinned slot).  A slot is reused
+    ``n_slots`` pushes later, after its previous copy has landed, so the bytes
+    ``wait`` returned stay valid until then."""
 
     def __init__(self, slot_bytes: int, n_slots: int = 2, device: torch.device | int | None = None):
         if slot_bytes <= 0 or n_slots <= 0:
@@ -56,11 +78,11 @@ class WireRing:
         self.slot_bytes = slot_bytes
         self.device = torch.device("cuda", torch.cuda.current_device() if device is None else
                                    torch.device(device).index or 0)
-        self.slots = [torch.empty(slot_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(n_slots)]
-        self.sizes = [0] * n_slots
-        self.done: list[torch.cuda.Event | None] = [None] * n_slots
-        self.stream = torch.cuda.Stream(device=self.device)
-        self.next = 0
+        self._ring = C.c_void_p()
+        with torch.cuda.device(self.device):
+            rc = N.lib().ztcp_wire_ring_create(slot_bytes, n_slots, C.byref(self._ring))
+        _raise(rc, "ztcp_wire_ring_create")
+        self._held: dict[int, torch.Tensor] = {}  # slot -> device blobs still being copied
 
     def push(self, blobs: torch.Tensor) -> int:
         if blobs.device != self.device or blobs.dtype != torch.uint8 or not blobs.is_contiguous():
@@ -68,24 +90,35 @@ class WireRing:
         n = blobs.numel()
         if n > self.slot_bytes:
             raise ValueError(f"{n} blob bytes exceed the slot size {self.slot_bytes}")
-        i = self.next
-        self.next = (i + 1) % len(self.slots)
-        if self.done[i] is not None:
-            self.done[i].synchronize()
-        ready = torch.cuda.Event()
-        ready.record(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(ready)
-            self.slots[i][:n].copy_(blobs.view(-1), non_blocking=True)
-            blobs.record_stream(self.stream)
-            ev = torch.cuda.Event()
-            ev.record(self.stream)
-        self.done[i] = ev
-        self.sizes[i] = n
-        return i
+        slot = C.c_int32(-1)
+        with torch.cuda.device(self.device):
+            rc = N.lib().ztcp_wire_ring_push(self._ring, C.c_void_p(blobs.data_ptr()), n,
+                                             _stream(self.device), C.byref(slot))
+        _raise(rc, "ztcp_wire_ring_push")
+        self._held[slot.value] = blobs  # the copy reads it on the ring's stream
+        return slot.value
 
     def wait(self, slot: int) -> torch.Tensor:
-        if self.done[slot] is None:
+        host, n = C.c_void_p(), C.c_size_t()
+        rc = N.lib().ztcp_wire_ring_wait(self._ring, slot, C.byref(host), C.byref(n))
+        if rc == N.EINVAL:
             raise ValueError(f"slot {slot} holds no copy")
-        self.done[slot].synchronize()
-        return self.slots[slot][:self.sizes[slot]]
+        _raise(rc, "ztcp_wire_ring_wait")
+        self._held.pop(slot, None)
+        if n.value == 0:
+            return torch.empty(0, dtype=torch.uint8)
+        buf = (C.c_uint8 * n.value).from_address(host.value)
+        return torch.from_numpy(np.ctypeslib.as_array(buf))
+
+    def close(self) -> None:
+        if self._ring:
+            rc = N.lib().ztcp_wire_ring_destroy(self._ring)
+            self._ring = C.c_void_p()
+            self._held.clear()
+            _raise(rc, "ztcp_wire_ring_destroy")
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
