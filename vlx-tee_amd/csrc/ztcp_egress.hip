@@ -13,9 +13,11 @@
 //     or 1 asym8 group) or a scale row (the 64 parameter bytes of one unit).
 //   * Eleven producer waves (on SIMDs 1-3; eight in the 12-wave kernels)
 //     take code rows in order from an LDS counter.  A code
-//     row quantizes its groups (loaded a row ahead), stages the scales in
-//     LDS, computes the keystream, XORs, and writes the ciphertext into a
-//     ring of row slots in LDS at its place in payload order.
+//     row quantizes its groups (loaded a row ahead; the int4 rows four lanes
+//     per page and transposed between the lanes of each quad afterwards),
+//     stages the scales in LDS, computes the keystream, XORs, and writes the
+//     ciphertext into a ring of row slots in LDS at its place in payload
+//     order.
 //   * A storer wave (wave 1, SIMD 1) stores every code row from the ring to
 //     the blobs, in payload order, transposed (four lanes per page, 64
 //     contiguous bytes per page per store).  After a unit's last code row
@@ -149,6 +151,68 @@ __device__ __forceinline__ void load_half(const EgressParams& p, const EgressPag
             cur.step(row.s.gpv, skip);
         }
     }
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// Pointer of lane 4k + M, read by every lane of quad k.
+template <int M>
+__device__ __forceinline__ const uint8_t* quad_ptr(const uint8_t* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = dpp32<M * 0x55>((uint32_t)v), hi = dpp32<M * 0x55>((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+// Half h of a code row with four lanes per page: load i (0..7) gives lane
+// 4k + q quad 4 (i / 4) + q of page 4k + i % 4, 64 contiguous bytes per
+// page per load; quad_untranspose then gives every lane its own page's
+// eight quads.  Needs the half's four chunks contiguous (groups per vector a
+// multiple of 4).
+__device__ __forceinline__ void load_half_t(const EgressParams& p, const EgressPage& pg, const Row& row, int h,
+                                            uint32_t (&w)[4][8]) {
+    const int ng = chunks_per_row(row.s.kind);
+    const uint8_t* src = row.s.src ? pg.v : pg.k;
+    const GroupCursor cur = group_cursor(row.u * row.s.nblk * ng + row.j * ng + 4 * h, row.s.gpv, row.s.col, p.head_dim);
+    const uint32_t q16 = (threadIdx.x & 3u) * 16u;
+    const uint8_t* pm[4] = {quad_ptr<0>(src), quad_ptr<1>(src), quad_ptr<2>(src), quad_ptr<3>(src)};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint4 v = ldg16(pm[i & 3] + cur.off + (uint32_t)(i >> 2) * 64u + q16, 0);
+        w[i >> 1][(i & 1) * 4 + 0] = v.x;
+        w[i >> 1][(i & 1) * 4 + 1] = v.y;
+        w[i >> 1][(i & 1) * 4 + 2] = v.z;
+        w[i >> 1][(i & 1) * 4 + 3] = v.w;
+    }
+}
+// 4 x 4 transpose of 16-byte quads between the registers and the lanes of
+// each lane quad: R0 = a[0..3], R1 = a[4..7], R2 = b[0..3], R3 = b[4..7];
+// afterwards lane m of the quad holds in Rq what lane q held in Rm.
+__device__ __forceinline__ void quad_transpose(uint32_t (&a)[8], uint32_t (&b)[8]) {
+    const bool b1 = (threadIdx.x >> 1) & 1u, b0 = threadIdx.x & 1u;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {  // (R0, R2), (R1, R3) with lane ^ 2
+        const uint32_t pa = dpp32<0x4E>(a[d]), pb = dpp32<0x4E>(b[d]);
+        const uint32_t na = b1 ? pb : a[d];
+        const uint32_t nb = b1 ? b[d] : pa;
+        a[d] = na;
+        b[d] = nb;
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {  // (R0, R1), (R2, R3) with lane ^ 1
+        const uint32_t pa0 = dpp32<0xB1>(a[d]), pa1 = dpp32<0xB1>(a[4 + d]);
+        const uint32_t pb0 = dpp32<0xB1>(b[d]), pb1 = dpp32<0xB1>(b[4 + d]);
+        const uint32_t na0 = b0 ? pa1 : a[d], na1 = b0 ? a[4 + d] : pa0;
+        const uint32_t nb0 = b0 ? pb1 : b[d], nb1 = b0 ? b[4 + d] : pb0;
+        a[d] = na0;
+        a[4 + d] = na1;
+        b[d] = nb0;
+        b[4 + d] = nb1;
+    }
+}
+__device__ __forceinline__ void quad_untranspose(uint32_t (&w)[4][8]) {
+    quad_transpose(w[0], w[1]);
+    quad_transpose(w[2], w[3]);
 }
 
 struct ProducerCtx {
@@ -297,11 +361,31 @@ __device__ __forceinline__ void quant_first(int32_t kind, const uint32_t (&w)[4]
 // chunks), which then arrive during the row's first double rounds.  Run at
 // the end of the previous row, whose last rounds cover the first half's
 // loads.
+// Whether a row's hot loads are made four lanes per page: the rows that read
+// 256 hot bytes per page (int4, int4 per 32) when each half is contiguous.
+// Loads of 16 bytes per lane from 64 pages touch 64 lines per instruction;
+// four lanes per page read 64 contiguous bytes of 16 pages.  On the rows of
+// all 256 workgroups at once this pattern reads 4.8 TB/s against 3.1 TB/s
+// (a probe of 16,384 pages); the int8 and e4m3 rows (128 bytes per page)
+// do not repay the transpose's VALU instructions.
+template <int FAM>
+__device__ __forceinline__ bool tq_row(const Row& row) {
+    return (row.s.gpv & 3) == 0 &&
+           ((FAM == 0 && row.s.kind == kSecInt4) || (FAM == 2 && row.s.kind == kSecInt4G32));
+}
+template <int FAM>
+__device__ __forceinline__ void load_half_any(const EgressParams& p, const EgressPage& pg, const Row& row, int h,
+                                              uint32_t (&w)[4][8]) {
+    if (tq_row<FAM>(row)) load_half_t(p, pg, row, h, w);
+    else load_half(p, pg, row, h, w);
+}
+
 template <int DT, int FAM>
 __device__ __forceinline__ void first_half(const EgressParams& p, const EgressPage& pg, const Row& row,
                                            uint32_t (&w)[4][8], uint32_t (&pt)[16], uint32_t (&sc)[4]) {
+    if (tq_row<FAM>(row)) quad_untranspose(w);
     quant_first<DT, FAM>(row.s.kind, w, pt, sc);
-    if (two_halves<FAM>(row.s.kind)) load_half(p, pg, row, 1, w);
+    if (two_halves<FAM>(row.s.kind)) load_half_any<FAM>(p, pg, row, 1, w);
 }
 
 // One code row.  pt / sc hold the row's first half quantized (first_half, at
@@ -326,6 +410,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     // the two quantizer calls into one store at a runtime index, which puts
     // sc in scratch memory
     uint32_t s2 = 0u, s3 = 0u;
+    if (tq_row<FAM>(row)) quad_untranspose(w);  // the second half (tq_row rows have two)
     if (kind == kSecInt4) {
         uint32_t t[2];
         quant_half<DT, 4>(w, pt + 8, t);
@@ -334,7 +419,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     } else if (FAM == 2 && kind == kSecInt4G32) {
         s2 = quant_half_int4g32<DT>(w, pt + 8);
     }
-    if (nxt.valid) load_half(p, c.pg, nxt, 0, w);
+    if (nxt.valid) load_half_any<FAM>(p, c.pg, nxt, 0, w);
     st.double_rounds<5>();
     if (kind != kSecRaw) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
@@ -415,7 +500,7 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     int32_t t = grab();
     Row cur = row_info(p.lay, t);
     if (cur.valid) {
-        load_half(p, c.pg, cur, 0, w);
+        load_half_any<FAM>(p, c.pg, cur, 0, w);
         first_half<DT, FAM>(p, c.pg, cur, w, pt, sc);
     }
 #pragma unroll 1
