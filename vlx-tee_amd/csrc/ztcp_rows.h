@@ -215,6 +215,49 @@ __device__ __forceinline__ void mac_rows(const Waiter& st, const uint32_t* ring,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Loads four lanes per page.  A load of 16 bytes per lane from 64 pages
+// touches 64 lines per instruction; four lanes per page read 64 contiguous
+// bytes of 16 pages.  The lanes of each quad then exchange their quads
+// (quad_transpose) so that every lane holds its own page's bytes.
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// Pointer of lane 4k + M, read by every lane of quad k.
+template <int M>
+__device__ __forceinline__ const uint8_t* quad_ptr(const uint8_t* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = dpp32<M * 0x55>((uint32_t)v), hi = dpp32<M * 0x55>((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+// 4 x 4 transpose of 16-byte quads between the registers and the lanes of
+// each lane quad: R0 = a[0..3], R1 = a[4..7], R2 = b[0..3], R3 = b[4..7];
+// afterwards lane m of the quad holds in Rq what lane q held in Rm.
+__device__ __forceinline__ void quad_transpose(uint32_t (&a)[8], uint32_t (&b)[8]) {
+    const bool b1 = (threadIdx.x >> 1) & 1u, b0 = threadIdx.x & 1u;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {  // (R0, R2), (R1, R3) with lane ^ 2
+        const uint32_t pa = dpp32<0x4E>(a[d]), pb = dpp32<0x4E>(b[d]);
+        const uint32_t na = b1 ? pb : a[d];
+        const uint32_t nb = b1 ? b[d] : pa;
+        a[d] = na;
+        b[d] = nb;
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {  // (R0, R1), (R2, R3) with lane ^ 1
+        const uint32_t pa0 = dpp32<0xB1>(a[d]), pa1 = dpp32<0xB1>(a[4 + d]);
+        const uint32_t pb0 = dpp32<0xB1>(b[d]), pb1 = dpp32<0xB1>(b[4 + d]);
+        const uint32_t na0 = b0 ? pa1 : a[d], na1 = b0 ? a[4 + d] : pa0;
+        const uint32_t nb0 = b0 ? pb1 : b[d], nb1 = b0 ? b[4 + d] : pb0;
+        a[d] = na0;
+        a[4 + d] = na1;
+        b[d] = nb0;
+        b[4 + d] = nb1;
+    }
+}
 // Row geometry of one section (all values wave-uniform).
 struct SecRows {
     int32_t kind, nblk, rpu, n_units;
