@@ -14,7 +14,7 @@
 //   * Eleven producer waves (on SIMDs 1-3; eight in the 12-wave kernels)
 //     take code rows in order from an LDS counter.  A code
 //     row quantizes its groups (loaded a row ahead; the int4 rows four lanes
-//     per page and transposed between the lanes of each quad afterwards),
+//     per page, transposed between the wave's 16-lane rows afterwards),
 //     stages the scales in LDS, computes the keystream, XORs, and writes the
 //     ciphertext into a ring of row slots in LDS at its place in payload
 //     order.
@@ -154,29 +154,28 @@ __device__ __forceinline__ void load_half(const EgressParams& p, const EgressPag
 }
 
 // Half h of a code row with four lanes per page: load i (0..7) gives lane
-// 4k + q quad 4 (i / 4) + q of page 4k + i % 4, 64 contiguous bytes per
-// page per load; quad_untranspose then gives every lane its own page's
-// eight quads.  Needs the half's four chunks contiguous (groups per vector a
-// multiple of 4).
+// 16 r + c quad 4 (i / 4) + r of page 16 (i % 4) + c, 64 contiguous bytes per
+// page per load; row_untranspose then gives every lane its own page's eight
+// quads.  Needs the half's four chunks contiguous (tq_row).
 __device__ __forceinline__ void load_half_t(const EgressParams& p, const EgressPage& pg, const Row& row, int h,
                                             uint32_t (&w)[4][8]) {
     const int ng = chunks_per_row(row.s.kind);
-    const uint8_t* src = row.s.src ? pg.v : pg.k;
     const GroupCursor cur = group_cursor(row.u * row.s.nblk * ng + row.j * ng + 4 * h, row.s.gpv, row.s.col, p.head_dim);
-    const uint32_t q16 = (threadIdx.x & 3u) * 16u;
-    const uint8_t* pm[4] = {quad_ptr<0>(src), quad_ptr<1>(src), quad_ptr<2>(src), quad_ptr<3>(src)};
+    const uint32_t r16 = (threadIdx.x >> 4 & 3u) * 16u;
+    const uint8_t* pm[4];
+    column_ptrs(row.s.src ? pg.v : pg.k, pm);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint4 v = ldg16(pm[i & 3] + cur.off + (uint32_t)(i >> 2) * 64u + q16, 0);
+        const uint4 v = ldg16(pm[i & 3] + cur.off + (uint32_t)(i >> 2) * 64u + r16, 0);
         w[i >> 1][(i & 1) * 4 + 0] = v.x;
         w[i >> 1][(i & 1) * 4 + 1] = v.y;
         w[i >> 1][(i & 1) * 4 + 2] = v.z;
         w[i >> 1][(i & 1) * 4 + 3] = v.w;
     }
 }
-__device__ __forceinline__ void quad_untranspose(uint32_t (&w)[4][8]) {
-    quad_transpose(w[0], w[1]);
-    quad_transpose(w[2], w[3]);
+__device__ __forceinline__ void row_untranspose(uint32_t (&w)[4][8]) {
+    row_transpose(w[0], w[1]);
+    row_transpose(w[2], w[3]);
 }
 
 struct ProducerCtx {
@@ -326,12 +325,9 @@ __device__ __forceinline__ void quant_first(int32_t kind, const uint32_t (&w)[4]
 // the end of the previous row, whose last rounds cover the first half's
 // loads.
 // Whether a row's hot loads are made four lanes per page: the rows that read
-// 256 hot bytes per page (int4, int4 per 32) when each half is contiguous.
-// Loads of 16 bytes per lane from 64 pages touch 64 lines per instruction;
-// four lanes per page read 64 contiguous bytes of 16 pages.  On the rows of
-// all 256 workgroups at once this pattern reads 4.8 TB/s against 3.1 TB/s
-// (a probe of 16,384 pages); the int8 and e4m3 rows (128 bytes per page)
-// do not repay the transpose's VALU instructions.
+// 256 hot bytes per page (int4, int4 per 32) when each half is four
+// contiguous chunks (groups per vector a multiple of 4).  The rows of 128
+// hot bytes per page (int8, e4m3, asym8) measured slower that way.
 template <int FAM>
 __device__ __forceinline__ bool tq_row(const Row& row) {
     return (row.s.gpv & 3) == 0 &&
@@ -347,7 +343,7 @@ __device__ __forceinline__ void load_half_any(const EgressParams& p, const Egres
 template <int DT, int FAM>
 __device__ __forceinline__ void first_half(const EgressParams& p, const EgressPage& pg, const Row& row,
                                            uint32_t (&w)[4][8], uint32_t (&pt)[16], uint32_t (&sc)[4]) {
-    if (tq_row<FAM>(row)) quad_untranspose(w);
+    if (tq_row<FAM>(row)) row_untranspose(w);
     quant_first<DT, FAM>(row.s.kind, w, pt, sc);
     if (two_halves<FAM>(row.s.kind)) load_half_any<FAM>(p, pg, row, 1, w);
 }
@@ -374,7 +370,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     // the two quantizer calls into one store at a runtime index, which puts
     // sc in scratch memory
     uint32_t s2 = 0u, s3 = 0u;
-    if (tq_row<FAM>(row)) quad_untranspose(w);  // the second half (tq_row rows have two)
+    if (two_halves<FAM>(kind) && tq_row<FAM>(row)) row_untranspose(w);  // the second half
     if (kind == kSecInt4) {
         uint32_t t[2];
         quant_half<DT, 4>(w, pt + 8, t);
