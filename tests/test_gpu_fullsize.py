@@ -3,7 +3,8 @@
 At these sizes the whole batch is checked through properties that do not need
 the oracle (every page verifies, a second encode is identical, tampering one
 page changes no other page's output) and a seeded sample of pages is checked
-byte for byte against the oracle (blobs and decoded pages).
+byte for byte against the oracle (blobs and decoded pages); a second test
+compares every page of every workload's batch with the oracle.
 
 * 1 GiB BF16 prefix, K8V4 + PRESERVE_FP8 (4096 tokens x 64 layers).
 * The same prefix under the reference's FP8_ONLY preset (int8 everywhere,
@@ -121,6 +122,46 @@ def test_full_prefix_roundtrip(pkg, O, W, name):
     _sample_vs_oracle(O, W, w, keys, k, v, blobs, ko, vo, th, seq, layers, _sample(w.n_pages, 7))
     import vlx_tee_amd.native_hip_codec as H
     assert H.device_diag() == 0
+
+
+@pytest.mark.parametrize("name", ["c2_k8v4_prefix1g", "c2_int4_prefix1g", "c4_mla_int4", "c3_fp8only_tamper",
+                                  "c2_k8v4asym_prefix1g", "c4_mla_int4g32", "c3_e4m3_tamper"])
+def test_full_prefix_every_page_vs_oracle(pkg, O, W, name):
+    """The whole 16,384-page batch byte for byte (the tamper workloads before
+    any tampering): every blob (codes, scales, ciphertext, tag) equals the
+    oracle encoder's and every decoded page equals the oracle decoder's, one
+    layer (its own layer id and first sequence nonce) per oracle call."""
+    import os
+    threads = max(1, min(16, os.cpu_count() or 1))
+    print(f"case {name}: encode", flush=True)
+    w, keys, k, v, th, seq, layers, blobs, geo = _encode(pkg, W, name)
+    rc, st, ko, vo = _decode(pkg, W, w, keys, blobs, th, seq, layers, geo, per_page=False)
+    assert rc == 0 and (st == 0).all()
+    ppl = w.pages_per_layer
+    for a in range(0, w.n_pages, ppl):
+        b = min(a + ppl, w.n_pages)
+        layer = int(layers[a])
+        assert (layers[a:b] == layer).all() and (seq[a:b] == seq[a] + np.arange(b - a, dtype=np.uint64)).all()
+        if a % (16 * ppl) == 0:
+            print(f"case {name}: pages {a}..{b - 1} vs oracle", flush=True)
+        want = O.egress_batch(_bits(k[a:b]), None if v is None else _bits(v[a:b]), th[a:b], dtype=O.BF16,
+                              preset=w.preset, rope_mode=w.rope_mode, rope_dim=w.rope_dim,
+                              expected_payload_bytes=w.payload_bytes, tenant_id_hash=W.TENANT_HASH,
+                              model_id_hash=W.MODEL_HASH, layer_id=layer, head_group_id=0,
+                              base_sequence_nonce=int(seq[a]), threads=threads, **keys)
+        got = blobs[a:b].cpu().numpy()
+        bad = np.nonzero((got != want).any(axis=1))[0]
+        assert bad.size == 0, f"pages {(a + bad[:8]).tolist()}: blob differs from the oracle"
+        orc, ost, ok, ov = O.ingress_batch(got, th[a:b], num_tokens=w.num_tokens, num_heads=w.num_heads,
+                                           head_dim=w.head_dim, rope_dim=w.rope_dim,
+                                           is_mla_single_buffer=w.mla, dtype=O.BF16,
+                                           expected_tenant_hash=W.TENANT_HASH,
+                                           expected_model_hash=W.MODEL_HASH, expected_layer_id=layer,
+                                           threads=threads, **keys)
+        assert orc == 0
+        assert np.array_equal(_bits(ko[a:b]), ok), f"layer {layer}: decoded K differs from the oracle"
+        if vo is not None:
+            assert np.array_equal(_bits(vo[a:b]), ov), f"layer {layer}: decoded V differs from the oracle"
 
 
 def _expected_verdict(byte):
