@@ -4,7 +4,8 @@
   host threads) keep their own verdicts: a tampered all-or-nothing batch still
   raises and is zeroed while a clean batch decodes, whatever the interleaving
   of their kernels (the reference keeps its status codes per call,
-  cpp:2056-2057 and cpp:2307, and zeroes in the same call, cpp:2481-2495).
+  cpp:2056-2057 and cpp:2307, and zeroes in the same call, cpp:2481-2495),
+  also when asynchronous calls in flight hold every other call slot.
 * A bounded wait that gives up (forced from the host: the wait limit set to
   zero polls, so each kernel's own wait expires and the kernel ends normally)
   fails closed: ingress returns ZTCP_EDEVICE and zeroes every output, per page
@@ -121,6 +122,54 @@ def test_two_threads_synchronous_calls(env, hip):
         msg, kb, vb = results["b"]
         assert msg == "ok"
         assert torch.equal(kb, e["ref_k"]) and torch.equal(vb, e["ref_v"])
+
+
+def test_synchronous_calls_with_every_other_slot_pending(env, hip):
+    """63 asynchronous calls held in flight behind a sleeping kernel take all
+    but one of the device's 64 call slots; two synchronous calls from two
+    threads then share the last one in turn (the second waits), and each
+    still returns its own verdict: a slot held by a call in progress is never
+    handed to another call."""
+    e = env
+    W, keys = e["W"], e["keys"]
+    s0 = torch.cuda.Stream()
+    n = 64
+    ko, vo = torch.empty_like(e["k"][:n]), torch.empty_like(e["v"][:n])
+    st = torch.empty((n,), dtype=torch.int32, device="cuda")
+    results = {}
+
+    def run(name, blobs, stream, barrier, ko_, vo_):
+        barrier.wait()
+        try:
+            with torch.cuda.stream(stream):
+                hip.fused_decode_cold_pages_peak_into(blobs, e["th"], ko_, vo_, e["w"].rope_dim, False,
+                                                      W.TENANT_HASH, W.MODEL_HASH, 0, keys["k0"], keys["k1"],
+                                                      keys["mk0"], keys["mk1"], keys["k2"], keys["k3"])
+            results[name] = ("ok", ko_, vo_)
+        except RuntimeError as ex:
+            results[name] = (str(ex), ko_, vo_)
+
+    for rep in range(3):
+        print(f"case 63 pending slots, repeat {rep}", flush=True)
+        results.clear()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s0):
+            torch.cuda._sleep(50_000_000)
+        for _ in range(63):
+            assert _ingress_async(e, e["blobs"][:n], ko, vo, st, s0) == 0
+        barrier = threading.Barrier(2)
+        outs = [(torch.full_like(e["k"], 3.0), torch.full_like(e["v"], 3.0)) for _ in range(2)]
+        ta = threading.Thread(target=run, args=("a", e["tampered"], torch.cuda.Stream(), barrier, *outs[0]))
+        tb = threading.Thread(target=run, args=("b", e["blobs"], torch.cuda.Stream(), barrier, *outs[1]))
+        ta.start(); tb.start(); ta.join(); tb.join()
+        torch.cuda.synchronize()
+        msg, ka, va = results["a"]
+        assert msg.startswith("KV_INTEGRITY_ERROR: Cold-page MAC verification failed"), msg
+        assert not ka.any() and not va.any()
+        msg, kb, vb = results["b"]
+        assert msg == "ok"
+        assert torch.equal(kb, e["ref_k"]) and torch.equal(vb, e["ref_v"])
+        assert (st.cpu().numpy() == 0).all()
 
 
 def test_expired_wait_fails_ingress_closed(env, hip):

@@ -8,6 +8,7 @@
 // the generic kernels (ztcp_generic.hip).
 #include <atomic>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "ztcp_params.h"
@@ -27,7 +28,8 @@ struct DeviceCtx {
     CallState* calls = nullptr;        // [kCallSlots], device
     CallState* host_calls = nullptr;   // [kCallSlots], pinned: verdict read-back
     hipEvent_t done[kCallSlots] = {};
-    bool busy[kCallSlots] = {};
+    bool busy[kCallSlots] = {};        // taken by a call
+    bool pending[kCallSlots] = {};     // released by an asynchronous call: free once done[k] completes
     int next = 0;
     int cu_count = 0;
 };
@@ -69,26 +71,38 @@ int device_ctx(DeviceCtx** out) {
     return ZTCP_OK;
 }
 
-// A free call slot: one never used, released, or whose asynchronous call's
-// event has completed.  When all are in flight, waits for the oldest.
+// A free call slot: one never used, released by a synchronous call, or
+// released by an asynchronous call whose event has completed.  A slot held by
+// a call still in progress is never handed out (its event is stale then).
+// When every slot is taken, waits for an asynchronous call to complete, or,
+// when synchronous calls in progress hold them all, for one of those to end.
 int acquire_call(DeviceCtx* c, int* slot) {
     std::unique_lock<std::mutex> lock(g_mu);
     for (;;) {
+        int wait_on = -1;
         for (int i = 0; i < kCallSlots; ++i) {
             const int k = (c->next + i) % kCallSlots;
             if (c->busy[k]) {
+                if (!c->pending[k]) continue;  // a call still holds it
                 const hipError_t q = hipEventQuery(c->done[k]);
-                if (q == hipErrorNotReady) continue;
+                if (q == hipErrorNotReady) {
+                    if (wait_on < 0) wait_on = k;
+                    continue;
+                }
                 if (q != hipSuccess) return ZTCP_EHIP;
             }
             c->busy[k] = true;
+            c->pending[k] = false;
             c->next = (k + 1) % kCallSlots;
             *slot = k;
             return ZTCP_OK;
         }
-        const hipEvent_t oldest = c->done[c->next];
         lock.unlock();
-        if (hipEventSynchronize(oldest) != hipSuccess) return ZTCP_EHIP;
+        if (wait_on >= 0) {
+            if (hipEventSynchronize(c->done[wait_on]) != hipSuccess) return ZTCP_EHIP;
+        } else {
+            std::this_thread::yield();
+        }
         lock.lock();
     }
 }
@@ -98,12 +112,16 @@ int acquire_call(DeviceCtx* c, int* slot) {
 int release_call(DeviceCtx* c, int slot, hipStream_t stream, bool async) {
     std::lock_guard<std::mutex> lock(g_mu);
     if (async) {
-        if (hipEventRecord(c->done[slot], stream) == hipSuccess) return ZTCP_OK;
+        if (hipEventRecord(c->done[slot], stream) == hipSuccess) {
+            c->pending[slot] = true;
+            return ZTCP_OK;
+        }
         // the event did not record: keep the slot out of use rather than
         // hand it to another call while this one may still write it
         return ZTCP_EHIP;
     }
     c->busy[slot] = false;
+    c->pending[slot] = false;
     return ZTCP_OK;
 }
 
