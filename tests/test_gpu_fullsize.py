@@ -16,6 +16,9 @@ compares every page of every workload's batch with the oracle.
 * The same three workloads as the task words them, with the extension kinds:
   K int8 asymmetric per 64 + e4m3 RoPE / V int4 per 32; FP8 e4m3 with 1% of
   the pages tampered; MLA latent int4 per 32 + e4m3 RoPE.
+* A paged KV pool: K, V and blob slots drawn independently from larger
+  pools, descriptors in shuffled order; same blobs and pages as the
+  contiguous batch.
 * The two small batches exactly as specified (64 and 256 pages of 16 tokens x
   4 KV heads x 128, INT4_SYM + PRESERVE_FP8, N(0,1) with RoPE columns x8 and
   1% of the channels x20, seed-7 keys, nonce = page index): every blob and
@@ -162,6 +165,77 @@ def test_full_prefix_every_page_vs_oracle(pkg, O, W, name):
         assert np.array_equal(_bits(ko[a:b]), ok), f"layer {layer}: decoded K differs from the oracle"
         if vo is not None:
             assert np.array_equal(_bits(vo[a:b]), ov), f"layer {layer}: decoded V differs from the oracle"
+
+
+_DESC = np.dtype([("k", "<u8"), ("v", "<u8"), ("blob", "<u8"), ("token_hash", "<i8"),
+                  ("sequence_nonce", "<u8"), ("layer_id", "<u2"), ("head_group_id", "<u2"),
+                  ("reserved", "<u4")])
+
+
+def _pool_descs(kpool, vpool, bpool, sk, sv, sb, th, seq, layers, order):
+    """Descriptor i for page order[i], whose K, V and blob sit in pool slots
+    sk / sv / sb of that page."""
+    pb = kpool[0].numel() * kpool.element_size()
+    j = order
+    d = np.zeros(len(order), dtype=_DESC)
+    d["k"] = np.uint64(kpool.data_ptr()) + sk[j].astype(np.uint64) * np.uint64(pb)
+    d["v"] = np.uint64(vpool.data_ptr()) + sv[j].astype(np.uint64) * np.uint64(pb)
+    d["blob"] = np.uint64(bpool.data_ptr()) + sb[j].astype(np.uint64) * np.uint64(bpool.size(1))
+    d["token_hash"] = th[j]
+    d["sequence_nonce"] = seq[j]
+    d["layer_id"] = layers[j]
+    return torch.from_numpy(d.view(np.uint8).reshape(len(order), _DESC.itemsize).copy()).to(kpool.device)
+
+
+def test_descriptors_over_a_scattered_pool(pkg, W):
+    """A paged KV pool: 2,048 pages of the K8V4 prefix (8 layers) whose K, V
+    and blob slots are drawn independently from pools three times as large,
+    with the descriptors in shuffled order (layers interleaved).  Egress and
+    ingress over those descriptors give exactly the blobs and pages of the
+    contiguous batch."""
+    import vlx_tee_amd.pages as P
+    print("case scattered pool: contiguous batch", flush=True)
+    w = W.WORKLOADS["c2_k8v4_prefix1g"]
+    n, dev = 2048, torch.device("cuda")
+    keys = W.session_keys()
+    k, v = W.generate(w, dev, torch.bfloat16, n_pages=n)
+    th, seq, layers = W.page_metadata(w, 0, n)
+    geo = dict(num_tokens=w.num_tokens, num_heads=w.num_heads, head_dim=w.head_dim, rope_dim=w.rope_dim,
+               dtype=torch.bfloat16, is_mla_single_buffer=False)
+    eg = dict(preset=w.preset, rope_mode=w.rope_mode, expected_payload_bytes=w.payload_bytes,
+              tenant_id_hash=W.TENANT_HASH, model_id_hash=W.MODEL_HASH, **geo, **keys)
+    ig = dict(expected_tenant_hash=W.TENANT_HASH, expected_model_hash=W.MODEL_HASH, per_page=False, **geo, **keys)
+    blobs = torch.empty((n, w.blob_bytes), dtype=torch.uint8, device=dev)
+    P.egress(P.build_descriptors(k, v, blobs, th, seq, layers), n, **eg)
+    ko, vo = torch.empty_like(k), torch.empty_like(v)
+    st = torch.full((n,), -1, dtype=torch.int32, device=dev)
+    assert P.ingress(P.build_descriptors(ko, vo, blobs, th, seq, layers), n, w.blob_bytes, page_status=st, **ig) == 0
+    torch.cuda.synchronize()
+
+    print("case scattered pool: descriptors over the pool", flush=True)
+    rng = np.random.default_rng(11)
+    slots = 3 * n
+    sk, sv, sb = (rng.permutation(slots)[:n] for _ in range(3))
+    order = rng.permutation(n)
+    kpool = torch.zeros((slots,) + tuple(k.shape[1:]), dtype=k.dtype, device=dev)
+    vpool = torch.zeros_like(kpool)
+    bpool = torch.zeros((slots, w.blob_bytes), dtype=torch.uint8, device=dev)
+    kpool[torch.from_numpy(sk).to(dev)] = k
+    vpool[torch.from_numpy(sv).to(dev)] = v
+    P.egress(_pool_descs(kpool, vpool, bpool, sk, sv, sb, th, seq, layers, order), n, **eg)
+    torch.cuda.synchronize()
+    assert torch.equal(bpool[torch.from_numpy(sb).to(dev)], blobs)
+
+    # decode from the pool's blob slots into other scattered slots
+    ok_s, ov_s = rng.permutation(slots)[:n], rng.permutation(slots)[:n]
+    kout = torch.full_like(kpool, 3.0)
+    vout = torch.full_like(vpool, 3.0)
+    st.fill_(-1)
+    d = _pool_descs(kout, vout, bpool, ok_s, ov_s, sb, th, seq, layers, order)
+    assert P.ingress(d, n, w.blob_bytes, page_status=st, **ig) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(kout[torch.from_numpy(ok_s).to(dev)], ko)
+    assert torch.equal(vout[torch.from_numpy(ov_s).to(dev)], vo)
 
 
 def _expected_verdict(byte):
