@@ -56,7 +56,46 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def run_gpu(wname: str, steps: int, warmup: int, settle_s: float) -> dict:
+# Phase-timer slots (TimerSlot in vlx-tee_amd/csrc/ztcp_rows.h).
+_TM = dict(mac_rows_begin=0, mac_first_row=1, mac_rows_end=2, mac_end=3, wg_end=4, prod_first_row=5,
+           prod_last=6, prod_busy=7, mac_wait=8, mac_miss=16, ring_wait=24, stage_wait=25, free_wait=26,
+           storer_wait=27, feed_wait=28, storer_end=29, feed_end=30, prod_waves=31, rows=32,
+           abs_start=40, abs_end=41, real_start=42, real_end=43)
+
+
+def summarize_phase_timers(rec) -> dict:
+    """Per-workgroup means of the phase-timer records of one launch (shader
+    clocks from the wave's leaving the first barrier), the shader clock rate
+    (s_memtime against the 100 MHz s_memrealtime) and the launch's spread."""
+    import numpy as np
+
+    r = rec.astype(np.float64)
+    col = lambda name, i=0: r[:, _TM[name] + i]  # noqa: E731
+    real = (col("real_end") - col("real_start")) / 1e8
+    ghz = float(np.mean((col("abs_end") - col("abs_start")) / np.maximum(real, 1e-12)) / 1e9)
+    waves = np.maximum(col("prod_waves"), 1)
+    m = lambda x: round(float(np.mean(x)), 1)  # noqa: E731
+    return dict(
+        workgroups=int(r.shape[0]), shader_ghz=round(ghz, 3),
+        start_spread_us=round(float((col("real_start").max() - col("real_start").min()) / 100), 2),
+        launch_span_us=round(float((col("real_end").max() - col("real_start").min()) / 100), 2),
+        wg_clocks=m(col("wg_end")), wg_clocks_max=round(float(col("wg_end").max()), 1),
+        mac=dict(rows_begin=m(col("mac_rows_begin")), first_row=m(col("mac_first_row")),
+                 rows_end=m(col("mac_rows_end")), end=m(col("mac_end")),
+                 wait_total=m(sum(col("mac_wait", i) for i in range(8))),
+                 wait_by_64_rows=[m(col("mac_wait", i)) for i in range(8)],
+                 rows_not_ready_by_64_rows=[m(col("mac_miss", i)) for i in range(8)]),
+        workers=dict(waves=m(col("prod_waves")), rows=m(col("rows")), first_row=m(col("prod_first_row")),
+                     last=m(col("prod_last")), busy_per_wave=m(col("prod_busy") / waves),
+                     ring_wait_per_wave=m(col("ring_wait") / waves),
+                     stage_wait_per_wave=m(col("stage_wait") / waves),
+                     free_wait_per_wave=m(col("free_wait") / waves)),
+        storer=dict(wait=m(col("storer_wait")), end=m(col("storer_end"))),
+        feeder=dict(wait=m(col("feed_wait")), end=m(col("feed_end"))),
+    )
+
+
+def run_gpu(wname: str, steps: int, warmup: int, settle_s: float, timers: bool = False) -> dict:
     import numpy as np
     import torch
 
@@ -166,6 +205,11 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float) -> dict:
     te = [a.elapsed_time(b) for a, b, _ in ev]
     ti = [b.elapsed_time(c) for _, b, c in ev]
     check_status("in the timed region")
+    phase = None
+    if timers:  # the records of the last step's two launches
+        import vlx_tee_amd._native as N
+        phase = dict(egress=summarize_phase_timers(N.phase_timers(0)),
+                     ingress=summarize_phase_timers(N.phase_timers(1)))
     hot = w.n_pages * w.hot_bytes_per_page
     wire = w.n_pages * w.blob_bytes
     me, mi = statistics.mean(te), statistics.mean(ti)
@@ -182,6 +226,8 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float) -> dict:
         settle=settle,
         device_diag=diag,
     )
+    if phase is not None:
+        res["phase_timers"] = phase
     del k, v, blobs, blobs_in, ko, vo
     torch.cuda.empty_cache()
     return res
@@ -482,9 +528,24 @@ def main() -> None:
     ap.add_argument("--no-wire", action="store_true", help="skip the wire-ring (device-to-host) measurement")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy kernel of BYTES (counter calibration)")
+    ap.add_argument("--phase-timers", action="store_true",
+                    help=("only print the per-phase clock breakdown of the workloads' fused kernels, "
+                          "from the timer build (libztcp_hip_timers.so); never a bench line"))
     a = ap.parse_args()
     if a.calibrate_copy:
         print(json.dumps(calibrate_copy(a.calibrate_copy, max(1, a.steps))))
+        return
+    if a.phase_timers:
+        _package()
+        import vlx_tee_amd._native as N
+        N.use_timer_library()
+        out = {}
+        for wn in [a.workload] + [x for x in a.also.split(",") if x and x != a.workload]:
+            r = run_gpu(wn, a.steps, a.warmup, a.settle_seconds, timers=True)
+            out[wn] = dict(egress_ms=round(r["egress_ms"], 4), ingress_ms=round(r["ingress_ms"], 4),
+                           phase_timers=r["phase_timers"])
+            _log(f"{wn}: {json.dumps(out[wn])}")
+        print(json.dumps(dict(phase_timers=out, build="libztcp_hip_timers.so")))
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the cold-page codec has no cross-GPU step "

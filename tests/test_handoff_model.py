@@ -41,9 +41,15 @@ def _const(fname, name):
     return int(m.group(1))
 
 
-NBLK = {"i8": 8, "i4": 4, "raw": 16}
+# code rows per unit of each section kind (code_rows_per_unit, ztcp_layout.h):
+# the reference's int8 / int4 / raw, and the extension kinds e4m3 (16-element
+# groups), int4 per 32 and int8 asymmetric per 64 (16 groups per unit, so 16
+# code rows and one parameter row).  Every kind but raw has one parameter row
+# per unit.
+NBLK = {"i8": 8, "i4": 4, "raw": 16, "e4": 8, "i4g32": 8, "a8": 16}
 LAZY_SCALE_ONLY_AT_END = False  # planted mistake: the storer publishes stored scale rows only when it is done
 IGNORE_STORER = False       # planted mistake: reuse a ring slot once the MAC wave alone has passed it
+FAM0_TASK_SPLIT = False     # planted mistake: ingress splits extension-kind tasks with the reference kinds' divisors
 CONFIGS = {  # sections (kind, units) of the layouts the kernels meet
     "k8v4": [("i8", 16), ("i8", 16), ("i4", 32)],
     "int4": [("i8", 16), ("i4", 16), ("i4", 32)],
@@ -52,6 +58,13 @@ CONFIGS = {  # sections (kind, units) of the layouts the kernels meet
     "raw_rope": [("raw", 4), ("i4", 8), ("i4", 16)],
     "tiny": [("i8", 1), ("i4", 1)],
     "one_unit_sections": [("i8", 1), ("i8", 3), ("i4", 2)],
+    # extension kinds (egress kind families 1 / 2, ingress family 1), the
+    # 16-token x 8-head x 128 pages and 64-token MLA pages of the workloads
+    "k8v4asym_e4rope": [("e4", 16), ("a8", 8), ("i4g32", 16)],
+    "e4m3": [("e4", 32), ("e4", 32)],
+    "mla_int4g32_e4rope": [("e4", 8), ("i4g32", 32)],
+    "asym8_small": [("a8", 1), ("a8", 3), ("i4g32", 2)],
+    "mixed_raw_ext": [("raw", 2), ("a8", 2), ("e4", 3)],
 }
 
 
@@ -89,16 +102,58 @@ class Sched:
                 continue
             if s == "blocked":
                 blocked += 1
-                if blocked > 50 * len(live) + 1000:
+                # with bounded waits every wait ends by itself
+                if BOUND is None and blocked > 50 * len(live) + 1000:
                     return False
             else:
                 blocked = 0
         raise RuntimeError("step limit")
 
 
+class Bounded:
+    """The kernels' bounded waits (wait_ge, vlx-tee_amd/csrc/ztcp_rows.h): a
+    wait gives up after `limit` polls, records the expiry in the workgroup's
+    LDS word and returns; with `short_circuit` (the kernels' rule) a wait that
+    finds the word set returns at its next poll.  After an expiry rows are
+    handed over out of turn, so the model's content checks no longer apply
+    (the kernel fails such a workgroup closed)."""
+
+    def __init__(self, limit, short_circuit=True):
+        self.limit, self.short_circuit = limit, short_circuit
+        self.expired = False
+        self.expiries = 0   # waits that ran out their own bound
+        self.polls = 0      # polls of all waits together
+
+    def wait(self, cond):
+        spins = 0
+        while not cond():
+            if self.short_circuit and self.expired:
+                return
+            if spins >= self.limit:
+                self.expired = True
+                self.expiries += 1
+                return
+            spins += 1
+            self.polls += 1
+            yield "blocked"
+
+
+BOUND = None  # a Bounded while a test runs the model with bounded waits
+
+
 def wait(cond):
+    if BOUND is not None:
+        yield from BOUND.wait(cond)
+        return
     while not cond():
         yield "blocked"
+
+
+def check(cond, *msg):
+    """The model's content checks; void once a bounded wait has expired."""
+    if BOUND is not None and BOUND.expired:
+        return
+    assert cond, msg
 
 
 def egress_model(secs, n_prod, seed):
@@ -138,12 +193,12 @@ def egress_model(secs, n_prod, seed):
                 yield from wait(lambda: stage_flag[g % KSTAGE] >= g - KSTAGE + 1)
                 if staged.get(g, 0) == 0:
                     stage_units[g % KSTAGE] = g
-                assert stage_units[g % KSTAGE] == g, "staging slot still holds another unit"
+                check(stage_units[g % KSTAGE] == g, "staging slot still holds another unit")
                 staged[g] = staged.get(g, 0) + 1
                 yield "ok"
             m = c["m"]
             yield from wait(lambda: slot_free(m))
-            assert ring_flag[m % KRING] <= max(0, m - KRING + 1), "ring slot overwritten before use"
+            check(ring_flag[m % KRING] <= max(0, m - KRING + 1), "ring slot overwritten before use")
             ring[m % KRING] = prow[m]
             yield "ok"
             ring_flag[m % KRING] = m + 1
@@ -159,7 +214,7 @@ def egress_model(secs, n_prod, seed):
                     yield "ok"
                 yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
                 yield "ok"  # the slot's quads are read ...
-                assert ring[m % KRING] == prow[m], ("storer read an overwritten slot", m, ring[m % KRING])
+                check(ring[m % KRING] == prow[m], ("storer read an overwritten slot", m, ring[m % KRING]))
             st["stored"] = m + 1  # ... before the release that frees it
             yield "ok"
             if prow[m][0] == "code":
@@ -167,8 +222,8 @@ def egress_model(secs, n_prod, seed):
                 kind = secs[si][0]
                 if kind != "raw" and j == NBLK[kind] - 1:
                     g = code[[c["m"] for c in code].index(m)]["g"]
-                    assert staged.get(g, 0) == per_unit[g], "scale row made before its unit was staged"
-                    assert stage_units[g % KSTAGE] == g
+                    check(staged.get(g, 0) == per_unit[g], "scale row made before its unit was staged")
+                    check(stage_units[g % KSTAGE] == g)
                     stage_flag[g % KSTAGE] = g + 1
                     made.append(g)
                     yield "ok"
@@ -191,7 +246,7 @@ def egress_model(secs, n_prod, seed):
                 gn = rows[i + 1][1]
                 yield from wait(lambda: gn in stored)
             yield from wait(lambda: slot_free(m))
-            assert ring_flag[m % KRING] <= max(0, m - KRING + 1)
+            check(ring_flag[m % KRING] <= max(0, m - KRING + 1))
             ring[m % KRING] = prow[m]
             yield "ok"
             ring_flag[m % KRING] = m + 1
@@ -200,7 +255,7 @@ def egress_model(secs, n_prod, seed):
     def mac():
         for m in range(len(prow)):
             yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
-            assert ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m])
+            check(ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m]))
             st["used"] = m + 1
             yield "ok"
 
@@ -235,14 +290,65 @@ def ingress_tasks(secs, L):
     return tasks
 
 
+def kernel_task(secs, t, L):
+    """Task t as the ingress kernel computes it (task_info, div_nblk, div_rpu
+    in ztcp_ingress.hip): integer arithmetic per section, with the divisors
+    chosen by the kind's code rows per unit (family 1: 8 -> /9, 4 -> /5,
+    otherwise /17; family 0 knows only int8 -> /9 and int4 -> /5)."""
+    fam1 = any(k not in ("i8", "i4", "raw") for k, _ in secs)
+    def div_nblk(x, kind):
+        return x // NBLK[kind]
+    def div_rpu(x, kind):
+        nblk = NBLK[kind]
+        if fam1 and not FAM0_TASK_SPLIT:
+            return x // 9 if nblk == 8 else (x // 5 if nblk == 4 else x // 17)
+        return x // 9 if kind == "i8" else x // 5
+    tb = cb = qb = m = 0
+    for kind, nu in secs:
+        nblk, quant = NBLK[kind], kind != "raw"
+        rpu = nblk + (1 if quant else 0)
+        n = nu * nblk + (nu if quant else 0)
+        if tb <= t < tb + n:
+            x = t - tb
+            scale, j = False, 0
+            if not quant:
+                u = div_nblk(x, kind)
+                j = x - u * nblk
+            else:
+                pre, full = min(L, nu), max(nu - L, 0)
+                if x < pre:
+                    scale, u = True, x
+                elif x - pre < full * rpu:
+                    x -= pre
+                    u = div_rpu(x, kind)
+                    r = x - u * rpu
+                    scale = r == nblk
+                    u, j = (u + L, 0) if scale else (u, r)
+                else:
+                    x -= pre + full * rpu
+                    u0 = div_nblk(x, kind)
+                    u, j = full + u0, x - u0 * nblk
+            if scale:
+                return dict(kind="scale", g=qb + u, m=m + nu * nblk + u)
+            return dict(kind="code", g=qb + u if quant else None, nblk=nblk, m=m + u * nblk + j, quant=quant)
+        tb += n
+        cb += nu * nblk
+        m += nu * nblk + (nu if quant else 0)
+        if quant:
+            qb += nu
+    return None
+
+
 def ingress_model(secs, n_dec, seed, padding=0):
     KRING = _const("ztcp_ingress.hip", "kRing")
     KSTAGE = _const("ztcp_ingress.hip", "kStage")
     L = _const("ztcp_ingress.hip", "kLookahead")
     prow = payload_rows(secs, padding)
-    tasks = ingress_tasks(secs, L)
+    # the decoders take tasks as the kernel computes them; the code rows they
+    # put into the ring must be exactly the payload's
+    tasks = [kernel_task(secs, t, L) for t in range(len(ingress_tasks(secs, L)))]
     code_m = {t["m"] for t in tasks if t["kind"] == "code"}
-    assert len(code_m) == sum(1 for r in prow if r[0] == "code")
+    check(len(code_m) == sum(1 for r in prow if r[0] == "code"))
     st = dict(task=0, used=0, stored=0)
     ring, ring_flag = [None] * KRING, [0] * KRING
 
@@ -268,7 +374,7 @@ def ingress_model(secs, n_dec, seed, padding=0):
             else:
                 m = k["m"]
                 yield from wait(lambda: st["used"] >= m - KRING + 1)
-                assert ring_flag[m % KRING] <= max(0, m - KRING + 1), "ring slot overwritten before use"
+                check(ring_flag[m % KRING] <= max(0, m - KRING + 1), "ring slot overwritten before use")
                 ring[m % KRING] = prow[m]
                 yield "ok"
                 ring_flag[m % KRING] = m + 1
@@ -276,7 +382,7 @@ def ingress_model(secs, n_dec, seed, padding=0):
                 if k["quant"]:
                     g = k["g"]
                     yield from wait(lambda: ready[g % KSTAGE] >= g + 1)
-                    assert stage[g % KSTAGE] == g, "code row read another unit's scales"
+                    check(stage[g % KSTAGE] == g, "code row read another unit's scales")
                     old = count[g % KSTAGE]; count[g % KSTAGE] += 1
                     yield "ok"
                     if old == k["nblk"] - 1:
@@ -290,7 +396,7 @@ def ingress_model(secs, n_dec, seed, padding=0):
             if m in code_m:
                 continue
             yield from wait(lambda: st["used"] >= m - KRING + 1)
-            assert ring_flag[m % KRING] <= max(0, m - KRING + 1)
+            check(ring_flag[m % KRING] <= max(0, m - KRING + 1))
             ring[m % KRING] = r
             yield "ok"
             ring_flag[m % KRING] = m + 1
@@ -299,7 +405,7 @@ def ingress_model(secs, n_dec, seed, padding=0):
     def verify():
         for m in range(len(prow)):
             yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
-            assert ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m])
+            check(ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m]))
             st["used"] = m + 1
             yield "ok"
 
@@ -355,5 +461,94 @@ def test_model_catches_a_staging_ring_smaller_than_the_lookahead():
     try:
         _const = lambda f, n: 1 if n == "kStage" else real(f, n)  # noqa: E731
         assert not ingress_model(CONFIGS["k8v4"], 3, 0)
+    finally:
+        _const = real
+
+
+@pytest.mark.parametrize("cfg", sorted(CONFIGS))
+def test_kernel_task_split_equals_the_decode_order(cfg):
+    """The kernel's integer task split (task_info) enumerates exactly the
+    decode order built unit by unit, for every kind's code rows per unit."""
+    L = _const("ztcp_ingress.hip", "kLookahead")
+    want = ingress_tasks(CONFIGS[cfg], L)
+    assert [kernel_task(CONFIGS[cfg], t, L) for t in range(len(want))] == want
+
+
+def test_model_catches_the_reference_divisors_on_extension_kinds():
+    """A planted mistake: splitting an asym8 section's tasks by 9 / 5 (the
+    reference kinds' rows per unit + 1) instead of 17 hands out code rows of
+    the wrong unit and scale rows at the wrong places; the model reports a
+    deadlock or a row the verify wave reads out of order."""
+    global FAM0_TASK_SPLIT
+    FAM0_TASK_SPLIT = True
+    try:
+        L = _const("ztcp_ingress.hip", "kLookahead")
+        secs = CONFIGS["k8v4asym_e4rope"]
+        want = ingress_tasks(secs, L)
+        assert [kernel_task(secs, t, L) for t in range(len(want))] != want
+        caught = 0
+        for seed in range(3):
+            try:
+                caught += not ingress_model(secs, 12, seed)
+            except AssertionError:
+                caught += 1
+        assert caught == 3
+    finally:
+        FAM0_TASK_SPLIT = False
+
+
+def _run_bounded(limit, short_circuit, model):
+    global BOUND
+    BOUND = Bounded(limit, short_circuit)
+    try:
+        done = model()
+        return done, BOUND
+    finally:
+        BOUND = None
+
+
+@pytest.mark.parametrize("cfg", ["k8v4", "k8v4asym_e4rope"])
+def test_bounded_waits_never_expire_in_a_healthy_workgroup(cfg):
+    for seed in range(2):
+        done, b = _run_bounded(10**6, True, lambda: egress_model(CONFIGS[cfg], 12, seed))
+        assert done and not b.expired
+        done, b = _run_bounded(10**6, True, lambda: ingress_model(CONFIGS[cfg], 12, seed))
+        assert done and not b.expired
+
+
+def test_one_expired_wait_ends_every_later_wait_of_the_workgroup():
+    """A planted deadlock (the storer holding back its stored scale rows) with
+    the kernels' bounded waits: the first wait to run out its bound marks the
+    workgroup, every other wait returns at its next poll, and the workgroup
+    finishes after at most one expiry per wave.  Without that rule each later
+    wait spins out its own bound again, so the time to failure grows with the
+    number of waits left (hundreds of bounds per wave in the kernel)."""
+    global LAZY_SCALE_ONLY_AT_END
+    LAZY_SCALE_ONLY_AT_END = True
+    n_prod, limit = 12, 400
+    waves = n_prod + 3  # producers, feeder, MAC wave, storer
+    try:
+        for seed in range(3):
+            done, b = _run_bounded(limit, True, lambda: egress_model(CONFIGS["k8v4"], n_prod, seed))
+            assert done and b.expired
+            assert 1 <= b.expiries <= waves
+            assert b.polls <= waves * limit
+            done, old = _run_bounded(limit, False, lambda: egress_model(CONFIGS["k8v4"], n_prod, seed))
+            assert done and old.expiries > 4 * waves
+            assert old.polls > 4 * waves * limit
+    finally:
+        LAZY_SCALE_ONLY_AT_END = False
+
+
+def test_one_expired_wait_ends_a_broken_ingress_workgroup():
+    """The same rule in the ingress hand-offs, on the planted staging ring
+    smaller than the look-ahead (a deadlock without bounded waits)."""
+    global _const
+    real = _const
+    try:
+        _const = lambda f, n: 1 if n == "kStage" else real(f, n)  # noqa: E731
+        for seed in range(3):
+            done, b = _run_bounded(400, True, lambda: ingress_model(CONFIGS["k8v4"], 12, seed))
+            assert done and b.expired and 1 <= b.expiries <= 14
     finally:
         _const = real

@@ -71,7 +71,21 @@ class PageDesc(C.Structure):
                 ("reserved", C.c_uint32)]
 
 
+# The phase-timer build of the same sources (vlx-tee_amd/build.py): the same
+# ABI plus ztcp_phase_timers_read (include/ztcp_timers.h).  Only a caller
+# that asks for it (bench.py --phase-timers) loads it, before any other use.
+TIMERS_LIB_PATH = Path(__file__).resolve().parent / "libztcp_hip_timers.so"
+
 _lib: C.CDLL | None = None
+
+
+def use_timer_library() -> None:
+    """Load the phase-timer build instead of the product library; must be
+    called before the library is first loaded."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != TIMERS_LIB_PATH:
+        raise RuntimeError("the product library is already loaded")
+    LIB_PATH = TIMERS_LIB_PATH
 
 
 def lib() -> C.CDLL:
@@ -83,6 +97,9 @@ def lib() -> C.CDLL:
         raise RuntimeError(
             f"HIP codec library missing: {LIB_PATH} (build it with python vlx-tee_amd/build.py)")
     L = C.CDLL(str(LIB_PATH))
+    if LIB_PATH == TIMERS_LIB_PATH:
+        L.ztcp_phase_timers_read.argtypes = [C.c_int32, C.c_void_p, C.c_int64]
+        L.ztcp_phase_timers_read.restype = C.c_int64
     P, G, A, K = C.c_void_p, C.POINTER(Geometry), C.POINTER(Aad), C.POINTER(Keys)
     i64, u64, u32, u16, i32 = C.c_int64, C.c_uint64, C.c_uint32, C.c_uint16, C.c_int
     for name in ("ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes"):
@@ -160,6 +177,24 @@ def _bind_keyring(L: C.CDLL) -> None:
         f = getattr(L, name)
         f.argtypes = args
         f.restype = res
+
+
+TIMER_SLOTS = 48  # include/ztcp_timers.h ZTCP_TIMER_SLOTS
+
+
+def phase_timers(direction: int):
+    """Phase-timer records of the last fused launch of `direction` (0 egress,
+    1 ingress) as a uint64 array [workgroups, TIMER_SLOTS] (timer build only)."""
+    import numpy as np
+
+    L = lib()
+    if not hasattr(L, "ztcp_phase_timers_read"):
+        raise RuntimeError("phase timers need the timer build (use_timer_library)")
+    buf = np.zeros(4096 * TIMER_SLOTS, dtype=np.uint64)
+    n = L.ztcp_phase_timers_read(direction, buf.ctypes.data, buf.size)
+    if n < 0:
+        raise RuntimeError(f"ztcp_phase_timers_read: {strerror(int(n))}")
+    return buf[:n].reshape(-1, TIMER_SLOTS)
 
 
 def strerror(code: int) -> str:

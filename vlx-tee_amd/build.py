@@ -1,9 +1,15 @@
 """Build the HIP C-ABI library ``libztcp_hip.so`` in-tree for gfx950.
 
 ``python vlx-tee_amd/build.py`` compiles every ``csrc/*.hip`` (device code)
-and ``csrc/*.cpp`` (host code: the session key ring) with hipcc into
-``vlx-tee_amd/libztcp_hip.so`` (exported symbols: include/ztcp.h and
-include/ztcp_keyring.h).
+and ``csrc/*.cpp`` (host code: the session key ring) with hipcc, one object
+per source in parallel, and links them into ``vlx-tee_amd/libztcp_hip.so``
+(exported symbols: include/ztcp.h and include/ztcp_keyring.h).
+
+It also builds ``libztcp_hip_timers.so``: the same sources with
+``-DZTCP_PHASE_TIMERS``, whose fused kernels record per-phase shader-clock
+counts (start-up, waits of each wave role, end) into a device buffer that
+``ztcp_phase_timers_read`` returns.  Only ``bench.py --phase-timers`` loads
+it; the product library carries no timer code.
 
 Flags: ``-ffp-contract=off`` and no fast-math (the quantizer's fp32 rounding
 order must match the reference's), packed-FP32 instructions disabled.
@@ -13,14 +19,17 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "libztcp_hip.so"
+LIB_TIMERS = HERE / "libztcp_hip_timers.so"
+OBJ = HERE / "_build"
 ARCH = os.environ.get("ZTCP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
@@ -31,16 +40,52 @@ def sources() -> list[Path]:
     return sorted((HERE / "csrc").glob("*.hip")) + sorted((HERE / "csrc").glob("*.cpp"))
 
 
-def build(verbose: bool = False) -> Path:
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc, *HIPCC_FLAGS, *map(str, sources()), "-o", str(tmp)]
+def _jobs() -> int:
+    n = os.cpu_count() or 4
+    return max(1, min(n, int(os.environ.get("MAX_JOBS", n)), 16))
+
+
+def _compile(hipcc: str, src: Path, obj: Path, defines: list[str], verbose: bool) -> None:
+    cmd = [hipcc, *HIPCC_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd))
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
+
+
+def _build_variant(hipcc: str, out: Path, variant: str, defines: list[str], verbose: bool,
+                   pool: ThreadPoolExecutor) -> list:
+    odir = OBJ / variant
+    odir.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    objs = [odir / (s.name + ".o") for s in srcs]
+    futs = [pool.submit(_compile, hipcc, s, o, defines, verbose) for s, o in zip(srcs, objs)]
+    return [futs, objs, out]
+
+
+def _link(hipcc: str, objs: list[Path], out: Path, verbose: bool) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd))
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False, timers: bool = True) -> Path:
+    """Compiles every source (always; no up-to-date check) and links the
+    product library, and with ``timers`` the phase-timer variant."""
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    variants = [("release", LIB, [])]
+    if timers:
+        variants.append(("timers", LIB_TIMERS, ["-DZTCP_PHASE_TIMERS=1"]))
+    with ThreadPoolExecutor(max_workers=_jobs()) as pool:
+        pending = [_build_variant(hipcc, out, name, defs, verbose, pool) for name, out, defs in variants]
+        for futs, objs, out in pending:
+            for f in futs:
+                f.result()
+            _link(hipcc, objs, out, verbose)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timers="--no-timers" not in sys.argv))

@@ -12,6 +12,10 @@
 #include <vector>
 
 #include "ztcp_params.h"
+#include "ztcp_rows.h"
+#ifdef ZTCP_PHASE_TIMERS
+#include "../../include/ztcp_timers.h"
+#endif
 
 using namespace ztcp;
 
@@ -125,6 +129,26 @@ int release_call(DeviceCtx* c, int slot, hipStream_t stream, bool async) {
     return ZTCP_OK;
 }
 
+#ifdef ZTCP_PHASE_TIMERS
+// Phase-timer records of the last fused launch per direction (diagnostic
+// build only): one buffer per direction, on the device of the first launch.
+static_assert(kTimerSlots == ZTCP_TIMER_SLOTS, "timer record size");
+unsigned long long* g_timer_buf[2] = {nullptr, nullptr};
+int64_t g_timer_wgs[2] = {0, 0};
+unsigned long long* timer_record(int dir, int64_t grid) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (grid > ZTCP_TIMER_MAX_WORKGROUPS) return nullptr;
+    if (!g_timer_buf[dir] &&
+        hipMalloc(&g_timer_buf[dir], sizeof(unsigned long long) * kTimerSlots * ZTCP_TIMER_MAX_WORKGROUPS) !=
+            hipSuccess)
+        return g_timer_buf[dir] = nullptr;
+    g_timer_wgs[dir] = grid;
+    return g_timer_buf[dir];
+}
+#else
+unsigned long long* timer_record(int, int64_t) { return nullptr; }
+#endif
+
 WaitSink wait_sink(DeviceCtx* c, CallState* call) {
     return WaitSink{&c->state->diag, call ? &call->diag : nullptr, g_spin_limit.load(std::memory_order_relaxed)};
 }
@@ -236,6 +260,7 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
 
     const bool fast = lay.aligned && expected_payload == (int64_t)lay.required && blob_bytes % 16 == 0 &&
                       (descs || (aligned16(k) && aligned16(v) && aligned16(blobs)));
+    if (fast) p.timers = timer_record(0, (batch + p.ppw - 1) / p.ppw);
     hipError_t e = fast ? launch_egress_fused(p, g->hot_dtype, stream)
                         : launch_egress_generic(p, g->hot_dtype, stream);
     return e == hipSuccess ? ZTCP_OK : ZTCP_EHIP;
@@ -339,6 +364,7 @@ hipError_t ingress_enqueue(IngressCall& c, CallState* call, int32_t* status, con
         own_status = e == hipSuccess;
     }
     if (e == hipSuccess) {
+        if (c.fast) p.timers = timer_record(1, (p.batch + p.ppw - 1) / p.ppw);
         e = c.fast ? launch_ingress_fused(p, c.dtype, stream) : launch_ingress_generic_impl(p, c.dtype, status, stream);
         if (e == hipSuccess && c.fast && !p.per_page) e = launch_ingress_finalize(p, stream);
     }
@@ -612,5 +638,23 @@ const char* ztcp_strerror(int code) {
 }
 
 const char* ztcp_last_error(void) { return t_last_error; }
+
+#ifdef ZTCP_PHASE_TIMERS
+int64_t ztcp_phase_timers_read(int32_t direction, uint64_t* out, int64_t max_words) {
+    if (direction < 0 || direction > 1 || (!out && max_words > 0)) return ZTCP_EINVAL;
+    if (hipDeviceSynchronize() != hipSuccess) return ZTCP_EHIP;
+    unsigned long long* buf = nullptr;
+    int64_t n = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        buf = g_timer_buf[direction];
+        n = g_timer_wgs[direction] * kTimerSlots;
+    }
+    if (!buf || n == 0) return 0;
+    if (n > max_words) return ZTCP_EINVAL;
+    if (hipMemcpy(out, buf, sizeof(uint64_t) * (size_t)n, hipMemcpyDeviceToHost) != hipSuccess) return ZTCP_EHIP;
+    return n;
+}
+#endif
 
 }  // extern "C"

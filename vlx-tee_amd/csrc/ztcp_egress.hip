@@ -75,9 +75,10 @@ constexpr int kFlagTask = kFlagStored + 1;            // next code row to hand o
 constexpr int kFlagExpired = kFlagTask + 1;           // 1: a bounded wait of the workgroup expired
 constexpr int kNumFlags = (kFlagExpired + 2) & ~1;    // even: the blob table after it is 8-byte aligned
 constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byte aligned)
-constexpr int kLdsWords = kLdsBlobs + 2 * 64;
+constexpr int kLdsTimers = kLdsBlobs + 2 * 64;        // phase-timer counters (timer builds only)
+constexpr int kLdsWords = kLdsTimers + kTimerLdsWords;
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
-static_assert(kLdsBlobs % 2 == 0, "blob table must be 8-byte aligned");
+static_assert(kLdsBlobs % 2 == 0 && kLdsTimers % 2 == 0, "blob table and timers must be 8-byte aligned");
 
 struct Row {
     int32_t valid;
@@ -384,7 +385,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     if (kind != kSecRaw) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
         uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;
-        wait_ge<kDiagEgressWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, c.wt);
+        wait_ge<kDiagEgressWait, kTmStageWait>(&flags[kFlagStage + row.g % kStage], row.g - kStage + 1, c.wt);
         // parameter words of this row: 2 (int8, e4m3, int4 per 32), 4 (int4)
         // or 1 (asym8), at logical words j * sw .. of this lane's page.  One
         // branch per count: a loop bounded by a runtime count would index sc
@@ -414,8 +415,8 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     for (int i = 0; i < 16; ++i) ks[i] ^= pt[i];
     pin_words(ks);
     uint32_t* slot = c.lds + (row.mrow % kRing) * kRowWords;
-    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, c.wt);
-    wait_ge<kDiagEgressWait>(&flags[kFlagStored], row.mrow - kRing + 1, c.wt);
+    wait_ge<kDiagEgressWait, kTmRingWait>(&flags[kFlagMacUsed], row.mrow - kRing + 1, c.wt);
+    wait_ge<kDiagEgressWait, kTmRingWait>(&flags[kFlagStored], row.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad(slot, c.lane, q, make_uint4(ks[4 * q], ks[4 * q + 1], ks[4 * q + 2], ks[4 * q + 3]));
@@ -434,7 +435,7 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     c.n2 = c.pg.nonce2;
     c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
-    c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+    c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
     const int32_t total = total_code_rows(p.lay);
     // The page descriptor and kernel argument loads above complete here,
     // before the loop: a load still counted as in flight where the loop
@@ -463,14 +464,25 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
         load_half_any<FAM>(p, c.pg, cur, 0, w);
         first_half<DT, FAM>(p, c.pg, cur, w, pt, sc);
     }
+    [[maybe_unused]] int32_t made = 0;
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
         set_row_priority(cur.mrow - used);
         const Row nxt = row_info(p.lay, tn);
         code_row<DT, FAM>(c, cur, nxt, w, pt, sc);
+        if constexpr (kPhaseTimers) {
+            if (made++ == 0) tm_min(c.wt.tm, kTmProdFirstRow, phase_clock() - c.wt.t0);
+        }
         t = tn;
         cur = nxt;
+    }
+    if constexpr (kPhaseTimers) {
+        const uint64_t now = phase_clock() - c.wt.t0;
+        tm_max(c.wt.tm, kTmProdLast, now);
+        tm_add(c.wt.tm, kTmProdBusy, now);
+        tm_add(c.wt.tm, kTmProdWaves, 1);
+        tm_add(c.wt.tm, kTmRows, (uint64_t)made);
     }
 }
 
@@ -509,7 +521,7 @@ struct MacPlan {
 };
 
 template <int DT>
-__device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds) {
+__device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32_t* lds, uint64_t t0) {
     const int lane = threadIdx.x & 63;
     const bool active = lane < ppw;
     const EgressPage pg = egress_page(p, page0 + (active ? lane : 0));
@@ -530,15 +542,18 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     m.init(p.lay);
     // Rows arrive in MAC order in the ring (code rows from the producers,
     // scale rows from the feeder), so the next row is always the next slot.
-    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsBegin, phase_clock() - t0);
     mac_rows<kRing, kDiagEgressWait>(wt, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
                                      m.total, [](int32_t, int, const uint4&) {});
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsEnd, phase_clock() - t0);
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     if (active)
         stg16(blob + kHeader + p.payload, 0,
               make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)));
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacEnd, phase_clock() - t0);
 }
 
 // Scale-row feeder (a wave on the MAC wave's SIMD, almost idle): copies each
@@ -552,7 +567,7 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
 // depends on a row that needs it to progress first.
 __device__ __forceinline__ void feed_load(const Waiter& wt, const uint32_t* lds, const uint8_t* src,
                                           int32_t g, uint4 (&x)[4]) {
-    wait_ge<kDiagEgressWait>(lds + kLdsFlags + kFlagScale + g % kScaleSlots, g + 1, wt);
+    wait_ge<kDiagEgressWait, kTmFeedWait>(lds + kLdsFlags + kFlagScale + g % kScaleSlots, g + 1, wt);
     if (src) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) x[q] = ldg16(src, q);
@@ -565,8 +580,8 @@ __device__ __forceinline__ void feed_load(const Waiter& wt, const uint32_t* lds,
 __device__ __forceinline__ void feed_put(const Waiter& wt, uint32_t* lds, const PageQuads& pq, int32_t rs,
                                          const uint4 (&x)[4]) {
     uint32_t* flags = lds + kLdsFlags;
-    wait_ge<kDiagEgressWait>(&flags[kFlagMacUsed], rs - kRing + 1, wt);
-    wait_ge<kDiagEgressWait>(&flags[kFlagStored], rs - kRing + 1, wt);
+    wait_ge<kDiagEgressWait, kTmFeedWait>(&flags[kFlagMacUsed], rs - kRing + 1, wt);
+    wait_ge<kDiagEgressWait, kTmFeedWait>(&flags[kFlagStored], rs - kRing + 1, wt);
     uint32_t* slot = lds + (rs % kRing) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
@@ -580,7 +595,7 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
     pq.init(lane);
     MacPlan m;
     m.init(p.lay);
-    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
     int32_t g0 = 0, r0 = 0;  // scale rows / MAC rows before the section
 #pragma unroll
     for (int si = 0; si < 3; ++si) {
@@ -601,6 +616,7 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
         g0 += n;
         r0 = rs + n;
     }
+    if constexpr (kPhaseTimers) tm_max(wt.tm, kTmFeedEnd, phase_clock() - wt.t0);
 }
 
 // Storer (one wave on SIMD 1): stores every code row from the ring to the
@@ -627,7 +643,7 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
     c.n2 = c.pg.nonce2;
     c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
-    c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+    c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
     c.init_stores(ppw);
     uint32_t* flags = lds + kLdsFlags;
     // a slot is reused only once stored: never let the producers sharing
@@ -653,7 +669,7 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
                 publish_scales(flags, pub, made);
                 pub = made;
             }
-            wait_ge<kDiagEgressWait>(f, r + 1, c.wt);
+            wait_ge<kDiagEgressWait, kTmStorerWait>(f, r + 1, c.wt);
             store_row(lds + (r % kRing) * kRowWords, c, (uint32_t)kHeader + 64u * (uint32_t)r);
             publish(&flags[kFlagStored], (uint32_t)r + 1u);  // the release orders the slot reads before it
             if (quant && (cr & (nblk - 1)) == nblk - 1) {
@@ -672,6 +688,7 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
         }
     }
     publish_scales(flags, pub, made);
+    if constexpr (kPhaseTimers) tm_max(c.wt.tm, kTmStorerEnd, phase_clock() - c.wt.t0);
 }
 
 // FAM 0: the reference's section kinds (int8, int4, raw); FAM 1: also e4m3
@@ -685,16 +702,19 @@ __global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(
     const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) lds[kLdsFlags + i] = 0u;
+    tm_clear(lds + kLdsTimers);
     if (threadIdx.x < 64) {
         uint64_t* blobs = reinterpret_cast<uint64_t*>(lds + kLdsBlobs);
         blobs[threadIdx.x] = (int)threadIdx.x < ppw ? reinterpret_cast<uint64_t>(egress_page(p, page0 + threadIdx.x).blob)
                                                     : 0ull;  // null past the last page
     }
     __syncthreads();
+    [[maybe_unused]] const uint64_t t0 = phase_clock();
+    [[maybe_unused]] const uint64_t rt0 = kPhaseTimers ? __builtin_amdgcn_s_memrealtime() : 0;
     const int wave = threadIdx.x >> 6;
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
-        egress_mac<DT>(p, page0, ppw, lds);
+        egress_mac<DT>(p, page0, ppw, lds, t0);
     } else if (wave == 4) {
         egress_scale_feed(p, lds);
     } else if ((wave & 3) == 0) {
@@ -710,6 +730,7 @@ __global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(
     // first 16 header bytes (magic 0: every ingress rejects the page with
     // status 1).  Same lanes, same addresses: the stores stay in order.
     __syncthreads();
+    tm_flush(lds + kLdsTimers, p.timers, t0, rt0);
     if (__hip_atomic_load(lds + kLdsFlags + kFlagExpired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u &&
         (int)threadIdx.x < ppw) {
         uint8_t* blob = reinterpret_cast<uint8_t*>(reinterpret_cast<const uint64_t*>(lds + kLdsBlobs)[threadIdx.x]);

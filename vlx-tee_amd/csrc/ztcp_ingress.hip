@@ -67,7 +67,8 @@ constexpr int kLdsPtrs = kLdsFlags + kNumFlags;      // [2][64] output pointers 
 constexpr int kLdsLayouts = kLdsPtrs + 2 * 2 * 64;   // [kNumLayouts] Layout, one per header flags value
 constexpr int kLayoutWords = (int)(sizeof(Layout) / 4);
 constexpr int kLdsHeaders = (kLdsLayouts + kNumLayouts * kLayoutWords + 3) & ~3;  // [64] 32-byte headers
-constexpr int kLdsWords = kLdsHeaders + 64 * 8;
+constexpr int kLdsTimers = kLdsHeaders + 64 * 8;       // phase-timer counters (timer builds only)
+constexpr int kLdsWords = kLdsTimers + kTimerLdsWords;
 static_assert(kLdsHeaders % 4 == 0, "header table must be 16-byte aligned");
 static_assert(sizeof(Layout) % 4 == 0, "Layout is copied word by word");
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
@@ -387,7 +388,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     uint32_t* flags = c.lds + kLdsFlags;
     // ciphertext to the verify wave, at its place in payload order
     uint32_t* slot = c.lds + (k.mrow % kRing) * kRowWords;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, c.wt);
+    wait_ge<kDiagIngressWait, kTmRingWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
@@ -403,7 +404,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     uint32_t sc[SW];
     if constexpr (KIND != kSecRaw) {
         const int slot_s = k.g % kStage;
-        wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, c.wt);
+        wait_ge<kDiagIngressWait, kTmStageWait>(&flags[kFlagReady + slot_s], k.g + 1, c.wt);
         const uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
         if constexpr (KIND == kSecInt8) {  // words 2j, 2j + 1 of the page's scale row
             const uint32_t* w = stage + quad_word(c.lane, k.j >> 1) + 2 * (k.j & 1);
@@ -474,7 +475,7 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
     const IngressParams& p = *c.p;
     uint32_t* flags = c.lds + kLdsFlags;
     uint32_t* slot = c.lds + (k.mrow % kRing) * kRowWords;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, c.wt);
+    wait_ge<kDiagIngressWait, kTmRingWait>(&flags[kFlagMacUsed], k.mrow - kRing + 1, c.wt);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
@@ -489,7 +490,7 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
     if (nxt.valid) load_block(c.pay + 64u * (uint32_t)nxt.block, ct);
     uint32_t sc[2];
     const int slot_s = k.g % kStage;
-    wait_ge<kDiagIngressWait>(&flags[kFlagReady + slot_s], k.g + 1, c.wt);
+    wait_ge<kDiagIngressWait, kTmStageWait>(&flags[kFlagReady + slot_s], k.g + 1, c.wt);
     const uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
     if constexpr (G::kParamWords == 2) {  // words 2j, 2j + 1 of the page's parameter row
         const uint32_t* w = stage + quad_word(c.lane, k.j >> 1) + 2 * (k.j & 1);
@@ -549,7 +550,7 @@ __device__ __forceinline__ void scale_task(const DecoderCtx& c, const Task& k, u
     if (nxt.valid) load_block(c.pay + 64u * (uint32_t)nxt.block, ct);
     if (params_nonfinite(sc)) flags[kFlagNaN + c.lane] = 1u;
     const int slot_s = k.g % kStage;
-    wait_ge<kDiagIngressWait>(&flags[kFlagFree + slot_s], k.g - kStage + 1, c.wt);
+    wait_ge<kDiagIngressWait, kTmFreeWait>(&flags[kFlagFree + slot_s], k.g - kStage + 1, c.wt);
     uint32_t* stage = c.lds + kLdsStage + slot_s * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -580,9 +581,13 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
     // the compiler wait for every outstanding memory operation wherever the
     // loop uses its result.
     __builtin_amdgcn_s_waitcnt(0);
+    [[maybe_unused]] int32_t made = 0;
 #pragma unroll 1
     while (t < total) {
         const int32_t tn = grab();
+        if constexpr (kPhaseTimers) {
+            if (made++ == 1) tm_min(c.wt.tm, kTmProdFirstRow, phase_clock() - c.wt.t0);
+        }
         // a scale row is as urgent as the first code row of its unit
         set_row_priority((k.scale ? (int32_t)(k.s.q_off / 64u) + k.u * k.s.nblk : k.mrow) - used);
         const Task nxt = task_info<FAM>(lay, tn);
@@ -605,6 +610,13 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
         t = tn;
         k = nxt;
     }
+    if constexpr (kPhaseTimers) {
+        const uint64_t now = phase_clock() - c.wt.t0;
+        tm_max(c.wt.tm, kTmProdLast, now);
+        tm_add(c.wt.tm, kTmProdBusy, now);
+        tm_add(c.wt.tm, kTmProdWaves, 1);
+        tm_add(c.wt.tm, kTmRows, (uint64_t)made);
+    }
 }
 
 // Feeder: copies every payload row that is not a code row of the workgroup
@@ -615,7 +627,7 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
 __device__ __forceinline__ void feed_put(const Waiter& wt, uint32_t* lds, const PageQuads& pq, int32_t r,
                                          const uint4 (&x)[4]) {
     uint32_t* flags = lds + kLdsFlags;
-    wait_ge<kDiagIngressWait>(&flags[kFlagMacUsed], r - kRing + 1, wt);
+    wait_ge<kDiagIngressWait, kTmFeedWait>(&flags[kFlagMacUsed], r - kRing + 1, wt);
     uint32_t* slot = lds + (r % kRing) * kRowWords;
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
@@ -626,7 +638,7 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
                              const uint8_t* pay, int lane) {
     PageQuads pq;
     pq.init(lane);
-    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
     const int32_t total = (int32_t)(p.payload / 64u);
     // payload rows [cb_i, ce_i) are section i's code rows (decoders)
     int32_t cb[3], ce[3];
@@ -650,6 +662,12 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
     };
     int32_t ra = next_fed(0);
     if (ra >= total) return;
+    struct FeedEnd {  // the feeder's end time, on every return path
+        const Waiter& w;
+        __device__ ~FeedEnd() {
+            if constexpr (kPhaseTimers) tm_max(w.tm, kTmFeedEnd, phase_clock() - w.t0);
+        }
+    } feed_end{wt};
     uint4 a[4], b[4];
     load(ra, a);
     int32_t rb = next_fed(ra + 1);
@@ -671,7 +689,7 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
 // come from the ring; its last (payload % 64) bytes and the tag are loaded
 // with the header.
 __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t page, uint32_t* lds, int lane,
-                                               const uint4 h0, const uint4 h1) {
+                                               const uint4 h0, const uint4 h1, uint64_t t0) {
     const uint8_t* blob = ingress_blob(p, page);
     const uint8_t* pay = blob + kHeader;
     const int32_t total = (int32_t)(p.payload / 64u);
@@ -689,10 +707,12 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     s.absorb_words<4>(hdr);
     PageQuads pq;
     pq.init(lane);
-    const Waiter st = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+    const Waiter st = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacRowsBegin, phase_clock() - t0);
     mac_rows<kRing, kDiagIngressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
                                       total, [](int32_t, int, const uint4&) {});
+    if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacRowsEnd, phase_clock() - t0);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
         if (i < ntail) s.absorb(tl[i]);
@@ -700,6 +720,7 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
     const uint32_t diff = (tag.x ^ (uint32_t)lo) | (tag.y ^ (uint32_t)(lo >> 32)) |
                           (tag.z ^ (uint32_t)hi) | (tag.w ^ (uint32_t)(hi >> 32));
+    if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacEnd, phase_clock() - t0);
     const uint32_t magic = h0.x & 0xFFFFu, version = (h0.x >> 16) & 0xFFu;
     if (magic != kMagic || version != kVersion) return 1;
     if (h0.y != p.exp_tenant || h0.z != p.exp_model || (h0.w & 0xFFFFu) != layer || lo64(h1) != tok) return 2;
@@ -729,6 +750,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     if (threadIdx.x < kNumLayouts) layouts[threadIdx.x] = ingress_layout(p, (int)threadIdx.x);
     uint32_t* flags = lds + kLdsFlags;
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) flags[i] = 0u;
+    tm_clear(lds + kLdsTimers);
     if (threadIdx.x < 64) {
         // Pages outside the row pipeline (another layout, invalid flags) get
         // its stores too: those of another layout are decoded again below,
@@ -740,6 +762,8 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         ptrs[64 + threadIdx.x] = reinterpret_cast<uint64_t>(v ? v : k);
     }
     __syncthreads();
+    [[maybe_unused]] const uint64_t t0 = phase_clock();
+    [[maybe_unused]] const uint64_t rt0 = kPhaseTimers ? __builtin_amdgcn_s_memrealtime() : 0;
     // every wave derives the workgroup layout from the 64 headers itself
     const uint4 h0 = hdrs[2 * lane], h1 = hdrs[2 * lane + 1];
     const int li = layout_index(p, h0.x);
@@ -749,7 +773,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     const Layout& lay = layouts[has_lay ? li_wg : 0];
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
-        flags[kFlagStatus + lane] = (uint32_t)verify_page(p, page, lds, lane, h0, h1);
+        flags[kFlagStatus + lane] = (uint32_t)verify_page(p, page, lds, lane, h0, h1, t0);
     } else if (wave == 4) {
         ingress_feed(p, lds, lay, has_lay, blob + kHeader, lane);
     } else if ((wave & 3) != 0 && has_lay) {  // waves 8 and 12 share SIMD 0 and idle
@@ -764,7 +788,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         c.tile = lds + kLdsTile + (wave - 1 - (wave >> 2)) * kRowWords;
         c.lane = lane;
         c.pq.init(lane);
-        c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired);
+        c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
         c.init_stores();
         decode_rows<DT, FAM>(c, lay);
     }
@@ -818,6 +842,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     const bool expired = flags[kFlagExpired] != 0u;
     if (expired && (int)threadIdx.x < ppw) flags[kFlagStatus + threadIdx.x] = (uint32_t)ZTCP_ERR_DEVICE;
     __syncthreads();
+    tm_flush(lds + kLdsTimers, p.timers, t0, rt0);
     if ((int)threadIdx.x < ppw) {
         const int32_t st = (int32_t)flags[kFlagStatus + threadIdx.x];
         const int64_t pg = page0 + threadIdx.x;

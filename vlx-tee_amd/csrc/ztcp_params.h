@@ -62,6 +62,7 @@ struct EgressParams {
     uint64_t base_seq;
     int32_t ppw;                   // pages per workgroup
     WaitSink sink;
+    unsigned long long* timers;    // phase-timer records, one per workgroup (timer builds; else nullptr)
 };
 
 struct IngressParams {
@@ -87,6 +88,7 @@ struct IngressParams {
     int32_t ppw;
     CallState* call;               // this call's failure word and diagnostics
     WaitSink sink;
+    unsigned long long* timers;    // phase-timer records, one per workgroup (timer builds; else nullptr)
 };
 
 // Page addressing (contiguous batch or descriptor array).

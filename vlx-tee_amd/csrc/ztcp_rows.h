@@ -49,40 +49,144 @@ __device__ __forceinline__ void lds_put_quad_at(uint32_t* row, uint32_t byte_off
     *reinterpret_cast<uint4*>(reinterpret_cast<char*>(row) + byte_off) = x;
 }
 
+// Phase timers (builds with ZTCP_PHASE_TIMERS only; the product library has
+// none of this code).  Each workgroup keeps kTimerSlots 64-bit counters in
+// LDS right after its other LDS data: shader-clock counts (s_memtime) of the
+// start-up, of the waits of each wave role and of the end, relative to the
+// clock at which the wave left the workgroup's first barrier.  Thread 0
+// copies them to the call's timer record at the end of the kernel.
+#ifdef ZTCP_PHASE_TIMERS
+constexpr bool kPhaseTimers = true;
+#else
+constexpr bool kPhaseTimers = false;
+#endif
+constexpr int kTimerSlots = 48;        // 64-bit counters per workgroup
+constexpr int kTimerLdsWords = kPhaseTimers ? 2 * kTimerSlots : 0;
+enum TimerSlot : int {
+    kTmMacRowsBegin = 0,   // MAC / verify wave: header absorbed, payload rows begin
+    kTmMacFirstRow = 1,    // MAC / verify wave: first payload row absorbed
+    kTmMacRowsEnd = 2,     // MAC / verify wave: last payload row absorbed
+    kTmMacEnd = 3,         // MAC / verify wave: tag done
+    kTmWgEnd = 4,          // after the workgroup's last barrier
+    kTmProdFirstRow = 5,   // earliest clock at which a producer / decoder published a row (min)
+    kTmProdLast = 6,       // latest clock at which a producer / decoder ran out of rows (max)
+    kTmProdBusy = 7,       // sum over producer / decoder waves of (exit - start)
+    kTmMacWait = 8,        // [8] MAC / verify wave: clocks waiting for a row, by payload row / 64
+    kTmMacMiss = 16,       // [8] MAC / verify wave: rows not ready when first tested, by row / 64
+    kTmRingWait = 24,      // producers / decoders: waiting for ring space
+    kTmStageWait = 25,     // egress producers: staging slot free; ingress decoders: scales ready
+    kTmFreeWait = 26,      // ingress scale rows: staging slot free
+    kTmStorerWait = 27,    // egress storer: waiting for a row
+    kTmFeedWait = 28,      // feeder: waiting (scale row stored, ring space)
+    kTmStorerEnd = 29,     // egress storer: done
+    kTmFeedEnd = 30,       // feeder: done
+    kTmProdWaves = 31,     // producer / decoder waves that ran
+    kTmRows = 32,          // rows made by producers / decoders
+    // written to the record by thread 0 directly
+    kTmAbsStart = 40,      // s_memtime after the first barrier
+    kTmAbsEnd = 41,        // s_memtime after the last barrier
+    kTmRealStart = 42,     // s_memrealtime (100 MHz) after the first barrier
+    kTmRealEnd = 43,       // s_memrealtime after the last barrier
+};
+
+__device__ __forceinline__ uint64_t phase_clock() {
+    if constexpr (kPhaseTimers) return __builtin_amdgcn_s_memtime();
+    return 0;
+}
+__device__ __forceinline__ void tm_add(uint32_t* tm, int slot, uint64_t v) {
+    if constexpr (kPhaseTimers) {
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(tm) + slot, (unsigned long long)v,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+__device__ __forceinline__ void tm_max(uint32_t* tm, int slot, uint64_t v) {
+    if constexpr (kPhaseTimers) {
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(tm) + slot, (unsigned long long)v,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+__device__ __forceinline__ void tm_min(uint32_t* tm, int slot, uint64_t v) {
+    if constexpr (kPhaseTimers) {
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_fetch_min(reinterpret_cast<unsigned long long*>(tm) + slot, (unsigned long long)v,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+// Clears the LDS counters (min slots start at all ones); every thread of the
+// workgroup calls it before the first barrier.
+__device__ __forceinline__ void tm_clear(uint32_t* tm) {
+    if constexpr (kPhaseTimers) {
+        if ((int)threadIdx.x < kTimerSlots)
+            reinterpret_cast<unsigned long long*>(tm)[threadIdx.x] =
+                threadIdx.x == kTmProdFirstRow ? ~0ull : 0ull;
+    }
+}
+// Thread 0, after the last barrier: the LDS counters and the absolute clocks
+// into this workgroup's record (kTimerSlots words) of the call's buffer.
+__device__ __forceinline__ void tm_flush(const uint32_t* tm, unsigned long long* rec, uint64_t start,
+                                         uint64_t real_start) {
+    if constexpr (kPhaseTimers) {
+        if (!rec || threadIdx.x != 0) return;
+        const uint64_t end = __builtin_amdgcn_s_memtime();
+        const uint64_t real_end = __builtin_amdgcn_s_memrealtime();
+        unsigned long long* r = rec + (size_t)blockIdx.x * kTimerSlots;
+        const unsigned long long* t = reinterpret_cast<const unsigned long long*>(tm);
+        for (int i = 0; i < kTimerSlots; ++i) r[i] = t[i];
+        r[kTmWgEnd] = end - start;
+        r[kTmAbsStart] = start;
+        r[kTmAbsEnd] = end;
+        r[kTmRealStart] = real_start;
+        r[kTmRealEnd] = real_end;
+    }
+}
+
 // Where a wave's bounded waits report an expiry: the device's sticky
 // diagnostics, the call's own diagnostics (ingress) and an LDS word of the
 // workgroup, which the kernel reads after its last barrier to fail every
-// page of the workgroup closed.
+// page of the workgroup closed.  `tm` and `t0` serve the phase timers only.
 struct Waiter {
     uint32_t* dev_diag;
     uint32_t* call_diag;   // nullptr: no per-call record
     uint32_t* expired;     // LDS
     uint32_t spin_limit;
+    uint32_t* tm;          // LDS phase-timer counters (timer builds)
+    uint64_t t0;           // clock at which the wave left the first barrier (timer builds)
 };
 
-__device__ __forceinline__ Waiter make_waiter(const WaitSink& s, uint32_t* expired_lds) {
-    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit};
+__device__ __forceinline__ Waiter make_waiter(const WaitSink& s, uint32_t* expired_lds, uint32_t* tm = nullptr,
+                                              uint64_t t0 = 0) {
+    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit, tm, t0};
 }
 
 // Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
 // Bounded: after spin_limit polls the wait records DIAG (device and call
 // diagnostics, the workgroup's LDS word) and returns; the caller carries on,
-// and the kernel fails the workgroup's pages at its end.
-template <uint32_t DIAG>
+// and the kernel fails the workgroup's pages at its end.  Once any wait of
+// the workgroup has expired, its hand-offs are broken and later waits may
+// never be satisfied: every wait that finds the LDS word set returns at its
+// next poll instead of spinning out its own bound, so a broken workgroup
+// ends about one bound after its first expiry.  TSLOT >= 0: timer builds add
+// the clocks spent here to that phase-timer slot.
+template <uint32_t DIAG, int TSLOT = -1>
 __device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, const Waiter& w) {
     if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
+    [[maybe_unused]] const uint64_t t_in = (kPhaseTimers && TSLOT >= 0) ? phase_clock() : 0;
     for (uint32_t spin = 0;; ++spin) {
+        if (__hip_atomic_load(w.expired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u) break;
         if (spin >= w.spin_limit) {
             if ((threadIdx.x & 63) == 0) {
                 atomicOr(w.dev_diag, DIAG);
                 if (w.call_diag) atomicOr(w.call_diag, DIAG);
             }
             __hip_atomic_store(w.expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            return;
+            break;
         }
         __builtin_amdgcn_s_sleep(1);
-        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) return;
+        if ((int32_t)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) break;
     }
+    if constexpr (kPhaseTimers && TSLOT >= 0) tm_add(w.tm, TSLOT, phase_clock() - t_in);
 }
 
 // Marks 16 words as produced here: the computation of w[] stays before the
@@ -149,15 +253,24 @@ __device__ __forceinline__ void mac_absorb(const Waiter& wt, const uint32_t* rin
                                            uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want,
                                            bool ready, OnQuad& on_quad, const MacRow& prev, bool has_prev) {
     if (__builtin_expect(!ready, 0)) {
+        [[maybe_unused]] const uint64_t t_in = phase_clock();
         wait_ge<DIAG>(ring_flags + r.slot, want, wt);
 #pragma unroll
         for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
+        if constexpr (kPhaseTimers) {
+            const int b = min((want - 1) >> 6, 7);
+            tm_add(wt.tm, kTmMacWait + b, phase_clock() - t_in);
+            tm_add(wt.tm, kTmMacMiss + b, 1);
+        }
     }
     s.absorb64_with(r.x, [&](int i) {
         if ((i & 1) == 0 && has_prev) on_quad(want - 2, i >> 1, prev.x[i >> 1]);
     });
     publish(used, (uint32_t)want);
+    if constexpr (kPhaseTimers) {
+        if (want == 1) tm_add(wt.tm, kTmMacFirstRow, phase_clock() - wt.t0);
+    }
 }
 
 // Every lane read the same flag word.  A vector compare and a ballot cost the
