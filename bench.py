@@ -126,7 +126,7 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float, timers: bool =
     def egress():
         P.egress(d_out, w.n_pages, preset=w.preset, rope_mode=w.rope_mode,
                  expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
-                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, **geo, **keys)
+                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, asynchronous=True, **geo, **keys)
 
     def ingress():
         P.ingress(d_in, w.n_pages, w.blob_bytes, expected_tenant_hash=TENANT_HASH,
@@ -259,7 +259,7 @@ def run_small_egress(wname: str, steps: int) -> dict:
     def egress():
         P.egress(d, w.n_pages, preset=w.preset, rope_mode=w.rope_mode,
                  expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
-                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, **geo, **keys)
+                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, asynchronous=True, **geo, **keys)
 
     egress()
     torch.cuda.synchronize()
@@ -326,7 +326,7 @@ def run_wire_ring(wname: str, parts: int = 4, reps: int = 3) -> dict:
     def egress(i):
         P.egress(d[i * q:(i + 1) * q], q, preset=w.preset, rope_mode=w.rope_mode,
                  expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
-                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, **geo, **keys)
+                 model_id_hash=MODEL_HASH, ext_layouts=w.extension, asynchronous=True, **geo, **keys)
 
     ring = SV.WireRing(q * w.blob_bytes, n_slots=2)
     copy_s, pipe_s = [], []

@@ -17,19 +17,23 @@
  *    `hot_dtype` (FP16 = the reference's only dtype, cpp:1499; BF16 = extension:
  *    the byte layout is unchanged, scales stay fp16 on the wire).
  *  - A blob is 32-byte header || payload || 16-byte tag (spec:17-51).
- *  - Calls are enqueued on `stream` (a hipStream_t; NULL = the default stream).
- *    Egress returns once enqueued.  Ingress without ZTCP_ASYNC synchronizes
- *    the stream and returns the reference's verdict; with ZTCP_ASYNC it
- *    returns after enqueueing and the verdict is read from `page_status`.
+ *  - Calls are enqueued on `stream` (a hipStream_t; NULL = the default stream)
+ *    and, like the reference's, are synchronous: they return once the work
+ *    is done, with its verdict.  With ZTCP_ASYNC (the entry points that take
+ *    flags) a call returns once enqueued: ingress verdicts are then read from
+ *    `page_status`, and an egress failure shows in the blobs (below).
  *  - Calls may overlap freely (several streams, several host threads): each
- *    ingress call keeps its failure record in device state of its own, which
- *    the call holds until its work on the stream has completed.
+ *    call keeps its failure record in device state of its own, which the call
+ *    holds until its work on the stream has completed.
  *  - Fail closed: the fused kernels' hand-offs use bounded waits.  If one
- *    expires (a device-side fault, never expected), ingress fails every page
- *    of the affected workgroup with ZTCP_ERR_DEVICE and zeroes its outputs, and
- *    a synchronous ingress returns ZTCP_EDEVICE; egress writes the affected
- *    workgroup's blobs with a zero header magic, which every ingress rejects
- *    (status 1).  Either way ztcp_device_diag reports it.
+ *    expires (a device-side fault, never expected), every later wait of the
+ *    same workgroup ends at once, ingress fails every page of the affected
+ *    workgroup with ZTCP_ERR_DEVICE and zeroes its outputs, and egress writes
+ *    the affected workgroup's blobs with a zero header magic, which every
+ *    ingress rejects (status 1).  A synchronous call then returns
+ *    ZTCP_EDEVICE, egress after zeroing every blob of the call (the
+ *    reference's wrapper zeroes out_blobs on any failure, nfc:597-600).
+ *    Either way ztcp_device_diag reports it.
  *  - Keys are passed by value and never retained (nfc:173-174 unpacks them
  *    into the same little-endian u64 words).
  *  - Errors are return codes, never exceptions: negative = argument / runtime
@@ -41,6 +45,16 @@
 
 #include <stddef.h>
 #include <stdint.h>
+
+/* Every entry point is exported from the library, which is built with hidden
+ * default visibility: the library exports exactly what its headers declare. */
+#ifndef ZTCP_API
+#if defined(__GNUC__) || defined(__clang__)
+#define ZTCP_API __attribute__((visibility("default")))
+#else
+#define ZTCP_API
+#endif
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -83,12 +97,15 @@ enum { ZTCP_HOT_FP16 = 0, ZTCP_HOT_BF16 = 1 };
 #define ZTCP_EOVERLAP (-2) /* an output aliases an input (cpp:1428-1437) */
 #define ZTCP_EHIP (-3)     /* the HIP runtime reported an error */
 #define ZTCP_EDEVICE (-4)  /* a kernel's bounded wait expired: outputs are zeroed
-                              (see ztcp_device_diag) */
+                              (ingress: all of them; egress: every blob of the
+                              call; see ztcp_device_diag) */
 #define ZTCP_ESCRATCH (-5) /* batch larger than ZTCP_NOALLOC_MAX_PAGES
                               (ztcp_ingress_peak_into_noalloc only) */
 
 /* Call flags. */
-#define ZTCP_ASYNC 0x1u          /* ingress: enqueue only; verdicts land in page_status */
+#define ZTCP_ASYNC 0x1u          /* enqueue only.  Ingress: verdicts land in page_status.
+                                    Egress: an expired wait shows only as blobs with a
+                                    zero header magic and in ztcp_device_diag */
 #define ZTCP_PER_PAGE 0x2u       /* ingress extension: keep verified pages, zero failing
                                     ones; default is the reference's all-or-nothing */
 #define ZTCP_EXT_LAYOUTS 0x4u    /* extension: the extension presets / RoPE mode.  Ingress
@@ -144,27 +161,27 @@ typedef struct ztcp_page_desc {
 /* Payload bytes padded to 4 (spec:203-246, what nfc passes as
  * expected_payload_bytes); (size_t)-1 for invalid preset / rope_mode.  The
  * extension presets 4..6 and RoPE mode 3 are sized as well. */
-size_t ztcp_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
+ZTCP_API size_t ztcp_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
 /* Unpadded minimum payload for header flags: required_payload_bytes_for_flags
  * (cpp:1439-1474); (size_t)-1 for invalid flags. */
-size_t ztcp_required_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
+ZTCP_API size_t ztcp_required_payload_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
 /* 32 + ztcp_payload_bytes + 16 (spec:248-250 cold_blob_bytes). */
-size_t ztcp_blob_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
+ZTCP_API size_t ztcp_blob_bytes(const ztcp_geometry* g, int64_t preset, int64_t rope_mode);
 
 /* Batch egress into a preallocated [batch, 32 + expected_payload_bytes + 16]
  * buffer.  Replaces fused_encode_cold_pages_peak_into_cpu (cpp:1904-2004):
  * page b is read at b * T*H*D elements, encoded with token_hashes[b] and
  * sequence_nonce = base_sequence_nonce + b, and written at b * blob_bytes.
  * Presets 1..3 and RoPE modes 0..2, as the reference (cpp:1947-1948). */
-int ztcp_egress_peak_into(const void* k_pages, const void* v_pages,
+ZTCP_API int ztcp_egress_peak_into(const void* k_pages, const void* v_pages,
                           const int64_t* page_token_hashes, uint8_t* out_blobs,
                           int64_t batch, const ztcp_geometry* g, int64_t preset,
                           int64_t rope_mode, int64_t expected_payload_bytes,
                           const ztcp_aad* aad, uint64_t base_sequence_nonce,
                           const ztcp_keys* keys, void* stream);
-/* The same with call flags: ZTCP_EXT_LAYOUTS admits the extension presets
- * 4..6 and RoPE mode 3 (no counterpart in the reference). */
-int ztcp_egress_peak_into_ext(const void* k_pages, const void* v_pages,
+/* The same with call flags: ZTCP_ASYNC; ZTCP_EXT_LAYOUTS admits the
+ * extension presets 4..6 and RoPE mode 3 (no counterpart in the reference). */
+ZTCP_API int ztcp_egress_peak_into_ext(const void* k_pages, const void* v_pages,
                               const int64_t* page_token_hashes, uint8_t* out_blobs,
                               int64_t batch, const ztcp_geometry* g, int64_t preset,
                               int64_t rope_mode, int64_t expected_payload_bytes,
@@ -174,13 +191,18 @@ int ztcp_egress_peak_into_ext(const void* k_pages, const void* v_pages,
 /* Descriptor form of the same egress for paged, multi-layer KV pools:
  * `pages` is a DEVICE array of n_pages descriptors; tenant and model hashes
  * come from `tenant_id_hash` / `model_id_hash`, every other header field from
- * the page's descriptor.  Same encoding as ztcp_egress_peak_into; `flags`:
- * ZTCP_EXT_LAYOUTS admits the extension presets / RoPE mode. */
-int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages,
+ * the page's descriptor.  Same encoding as ztcp_egress_peak_into. */
+ZTCP_API int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages,
                       const ztcp_geometry* g, int64_t preset, int64_t rope_mode,
                       int64_t expected_payload_bytes, uint32_t tenant_id_hash,
-                      uint32_t model_id_hash, const ztcp_keys* keys, uint32_t flags,
-                      void* stream);
+                      uint32_t model_id_hash, const ztcp_keys* keys, void* stream);
+/* The same with call flags: ZTCP_ASYNC, ZTCP_EXT_LAYOUTS (the extension
+ * presets / RoPE mode). */
+ZTCP_API int ztcp_egress_batch_ext(const ztcp_page_desc* pages, int64_t n_pages,
+                          const ztcp_geometry* g, int64_t preset, int64_t rope_mode,
+                          int64_t expected_payload_bytes, uint32_t tenant_id_hash,
+                          uint32_t model_id_hash, const ztcp_keys* keys, uint32_t flags,
+                          void* stream);
 
 /* Batch ingress into preallocated outputs.  Replaces
  * fused_decode_cold_pages_peak_into_cpu (cpp:2250-2496): every page is
@@ -191,7 +213,7 @@ int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages,
  * failing page is returned (ZTCP_EDEVICE when a bounded wait expired).
  * page_status (DEVICE int32[batch], may be NULL) receives every page's
  * verdict (0..4). */
-int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
+ZTCP_API int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
                            const int64_t* expected_token_hashes, void* out_k_pages,
                            void* out_v_pages, int64_t batch, const ztcp_geometry* g,
                            uint32_t expected_tenant_hash, uint32_t expected_model_hash,
@@ -208,9 +230,13 @@ int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
  * batches are limited to ZTCP_NOALLOC_MAX_PAGES pages (ZTCP_ESCRATCH beyond).
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other threads) race and must be serialized by the caller.
- * The array is set up on the first call on each device. */
+ * The array is set up on the first call on each device.  Only a ZTCP_ASYNC
+ * call can be recorded into a HIP graph (a synchronous one copies its verdict
+ * to the host and waits for the stream): a synchronous call on a stream under
+ * capture returns ZTCP_EINVAL.  ztcp_device_diag reads this path's sticky
+ * diagnostics without allocating. */
 #define ZTCP_NOALLOC_MAX_PAGES 65536
-int ztcp_ingress_peak_into_noalloc(const uint8_t* cold_blobs, int64_t blob_bytes,
+ZTCP_API int ztcp_ingress_peak_into_noalloc(const uint8_t* cold_blobs, int64_t blob_bytes,
                                    const int64_t* expected_token_hashes, void* out_k_pages,
                                    void* out_v_pages, int64_t batch, const ztcp_geometry* g,
                                    uint32_t expected_tenant_hash, uint32_t expected_model_hash,
@@ -219,7 +245,7 @@ int ztcp_ingress_peak_into_noalloc(const uint8_t* cold_blobs, int64_t blob_bytes
 
 /* Descriptor form of the same ingress (blob in, k/v out; the expected token
  * hash and layer id of each page come from its descriptor). */
-int ztcp_ingress_batch(const ztcp_page_desc* pages, int64_t n_pages, int64_t blob_bytes,
+ZTCP_API int ztcp_ingress_batch(const ztcp_page_desc* pages, int64_t n_pages, int64_t blob_bytes,
                        const ztcp_geometry* g, uint32_t expected_tenant_hash,
                        uint32_t expected_model_hash, const ztcp_keys* keys,
                        int32_t* page_status, uint32_t flags, void* stream);
@@ -228,9 +254,9 @@ int ztcp_ingress_batch(const ztcp_page_desc* pages, int64_t n_pages, int64_t blo
  * (cpp:2499-2524): dst = src ^ ChaCha20(key, nonce, counter..).
  * ztcp_siphash128 replaces siphash24_128_cpu (cpp:2526-2538).  key, nonce
  * are HOST byte arrays; data and outputs are DEVICE pointers. */
-int ztcp_chacha20_xor(const uint8_t* src, uint8_t* dst, size_t len, const uint8_t key[32],
+ZTCP_API int ztcp_chacha20_xor(const uint8_t* src, uint8_t* dst, size_t len, const uint8_t key[32],
                       uint32_t initial_counter, const uint8_t nonce[12], void* stream);
-int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
+ZTCP_API int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
                     uint8_t* tag16, void* stream);
 
 /* Self-check of the device arithmetic the fused quantizer relies on: for
@@ -243,11 +269,12 @@ int ztcp_siphash128(const uint8_t* data, size_t len, uint64_t mk0, uint64_t mk1,
  * its neighbours and all 256 codes.  Returns the number of violations
  * (0 = pass) or a negative error.  A test hook like the
  * reference's (cpp:2499-2538); it has no counterpart of its own there. */
-int ztcp_selftest(void);
+ZTCP_API int ztcp_selftest(void);
 
 /* Device-side diagnostics of the current device: returns and clears the
- * sticky flags a kernel's bounded waits set (0 = none). Synchronizes. */
-int ztcp_device_diag(void);
+ * sticky flags a kernel's bounded waits set (0 = none).  Synchronizes; sets
+ * nothing up and allocates nothing. */
+ZTCP_API int ztcp_device_diag(void);
 
 /* Test hook for the fail-closed paths (no counterpart in the reference):
  * sets the number of polls after which the fused kernels' bounded waits give
@@ -255,7 +282,7 @@ int ztcp_device_diag(void);
  * (about 30 ms).  n = 0 makes every wait that is not already satisfied expire
  * at once, so a test can drive the expiry handling to completion without a
  * fault.  Returns the previous value. */
-int64_t ztcp_debug_spin_limit(int64_t n);
+ZTCP_API int64_t ztcp_debug_spin_limit(int64_t n);
 
 /* Serving-side steps around the codec (vlx-tee_amd/csrc/ztcp_serving.hip).
  *
@@ -268,7 +295,7 @@ int64_t ztcp_debug_spin_limit(int64_t n);
  * writes it.  packed = 0: out is DEVICE uint8[n], 1 where the verdict is 0;
  * packed = 1: out is DEVICE uint8[(n + 7) / 8], page i in bit i % 8 of byte
  * i / 8 (least significant bit first), trailing bits 0.  Enqueued on stream. */
-int ztcp_hit_bitmap(const int32_t* page_status, int64_t n, uint8_t* out, int32_t packed, void* stream);
+ZTCP_API int ztcp_hit_bitmap(const int32_t* page_status, int64_t n, uint8_t* out, int32_t packed, void* stream);
 
 /* Egress wire ring: a batch of blobs leaves HBM into the next of n_slots
  * pinned host slots, on a copy stream of the ring's own that waits for the
@@ -286,19 +313,19 @@ int ztcp_hit_bitmap(const int32_t* page_status, int64_t n, uint8_t* out, int32_t
  *            give its bytes (HOST memory owned by the ring).
  *   destroy: waits for the copies in flight, then frees the ring. */
 typedef struct ztcp_wire_ring ztcp_wire_ring;
-int ztcp_wire_ring_create(size_t slot_bytes, int32_t n_slots, ztcp_wire_ring** ring);
-int ztcp_wire_ring_push(ztcp_wire_ring* ring, const uint8_t* blobs, size_t nbytes, void* stream,
+ZTCP_API int ztcp_wire_ring_create(size_t slot_bytes, int32_t n_slots, ztcp_wire_ring** ring);
+ZTCP_API int ztcp_wire_ring_push(ztcp_wire_ring* ring, const uint8_t* blobs, size_t nbytes, void* stream,
                         int32_t* slot);
-int ztcp_wire_ring_wait(ztcp_wire_ring* ring, int32_t slot, const uint8_t** host, size_t* nbytes);
-int ztcp_wire_ring_destroy(ztcp_wire_ring* ring);
+ZTCP_API int ztcp_wire_ring_wait(ztcp_wire_ring* ring, int32_t slot, const uint8_t** host, size_t* nbytes);
+ZTCP_API int ztcp_wire_ring_destroy(ztcp_wire_ring* ring);
 
 /* Short description of a return code. */
-const char* ztcp_strerror(int code);
+ZTCP_API const char* ztcp_strerror(int code);
 
 /* Why the calling thread's last call returned ZTCP_EINVAL or ZTCP_EOVERLAP:
  * the reference's TORCH_CHECK message for the same condition where it has
  * one ("" when the last call succeeded). */
-const char* ztcp_last_error(void);
+ZTCP_API const char* ztcp_last_error(void);
 
 #ifdef __cplusplus
 }

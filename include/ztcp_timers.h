@@ -17,6 +17,16 @@
 
 #include <stdint.h>
 
+/* Every entry point is exported from the library, which is built with hidden
+ * default visibility: the library exports exactly what its headers declare. */
+#ifndef ZTCP_API
+#if defined(__GNUC__) || defined(__clang__)
+#define ZTCP_API __attribute__((visibility("default")))
+#else
+#define ZTCP_API
+#endif
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -29,7 +39,7 @@ extern "C" {
  * after synchronizing the device.  Returns the number of words written
  * (workgroups * ZTCP_TIMER_SLOTS), 0 when no fused launch was recorded, or a
  * negative ZTCP_E* code. */
-int64_t ztcp_phase_timers_read(int32_t direction, uint64_t* out, int64_t max_words);
+ZTCP_API int64_t ztcp_phase_timers_read(int32_t direction, uint64_t* out, int64_t max_words);
 
 #ifdef __cplusplus
 }

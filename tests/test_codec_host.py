@@ -90,3 +90,25 @@ def test_hit_bitmap_rejects_bad_verdict_tensors(pkg):
         SV.hit_bitmap(torch.zeros((2, 2), dtype=torch.int32))
     with pytest.raises(ValueError, match="device tensor"):
         SV.hit_bitmap(torch.zeros(4, dtype=torch.int32))
+
+
+def test_wire_ring_views_keep_the_slot_memory_alive(pkg):
+    """A host view that WireRing.wait returned is the ring's pinned slot
+    memory: the ring is destroyed only after the ring object and every such
+    view are gone (modelled here with host memory and a recording destroy)."""
+    import ctypes as C
+    import gc
+
+    import vlx_tee_amd.serving as SV
+
+    freed = []
+    mem = (C.c_uint8 * 64)(*range(64))
+    h = SV._RingHandle(C.c_void_p(1), destroy=freed.append)
+    view = SV._host_view(C.addressof(mem), 64, h)[8:24]
+    del h  # the ring object lets go (close / garbage collection)
+    gc.collect()
+    assert not freed, "the ring was freed while a view of its slot was alive"
+    assert view.tolist() == list(range(8, 24))
+    del view
+    gc.collect()
+    assert len(freed) == 1

@@ -220,17 +220,33 @@ def test_expired_wait_fails_ingress_closed(env, hip):
 
 
 def test_expired_wait_fails_egress_closed(env, hip):
-    """Egress whose waits give up writes blobs with a zero header magic: every
-    page is rejected by ingress with status 1 (cpp:2313-2316)."""
+    """Egress whose waits give up fails closed.  Synchronous (the reference's
+    form): the call raises KV_INTEGRITY_ERROR with every blob zeroed, before
+    any caller could commit the batch (nfc:597-600 zeroes out_blobs on any
+    failure).  Asynchronous: the call returns once enqueued, and the blobs of
+    the affected workgroups carry a zero header magic, which every ingress
+    rejects with status 1 (cpp:2313-2316)."""
     e = env
-    W, keys, w = e["W"], e["keys"], e["w"]
-    print("case expired egress wait", flush=True)
-    blobs = torch.empty_like(e["blobs"])
+    N, W, keys, w = e["N"], e["W"], e["keys"], e["w"]
+    print("case expired egress wait, synchronous", flush=True)
+    blobs = torch.full_like(e["blobs"], 0xA5)
     prev = hip.debug_spin_limit(0)
     try:
-        hip.fused_encode_cold_pages_peak_into(e["k"], e["v"], e["th"], blobs, w.preset, w.rope_mode, w.rope_dim,
-                                              w.payload_bytes, W.TENANT_HASH, W.MODEL_HASH, 0, 0, 0, keys["k0"],
-                                              keys["k1"], keys["mk0"], keys["mk1"], keys["k2"], keys["k3"])
+        with pytest.raises(RuntimeError, match="^KV_INTEGRITY_ERROR: device-side bounded wait expired"):
+            hip.fused_encode_cold_pages_peak_into(e["k"], e["v"], e["th"], blobs, w.preset, w.rope_mode,
+                                                  w.rope_dim, w.payload_bytes, W.TENANT_HASH, W.MODEL_HASH, 0, 0,
+                                                  0, keys["k0"], keys["k1"], keys["mk0"], keys["mk1"], keys["k2"],
+                                                  keys["k3"])
+        assert not blobs.any(), "every blob of the failed call is zeroed"
+        print("case expired egress wait, asynchronous", flush=True)
+        blobs.fill_(0xA5)
+        g = N.geometry(w.num_tokens, w.num_heads, w.head_dim, w.rope_dim, N.HOT_BF16, False)
+        aad = N.Aad(W.TENANT_HASH, W.MODEL_HASH, 0, 0)
+        rc = N.lib().ztcp_egress_peak_into_ext(
+            e["k"].data_ptr(), e["v"].data_ptr(), e["th"].data_ptr(), blobs.data_ptr(), N_PAGES, C.byref(g),
+            w.preset, w.rope_mode, w.payload_bytes, C.byref(aad), 0, C.byref(N.keys(**keys)), N.ASYNC,
+            C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == N.OK
         torch.cuda.synchronize()
     finally:
         hip.debug_spin_limit(prev)
@@ -244,6 +260,58 @@ def test_expired_wait_fails_egress_closed(env, hip):
                                               keys["k2"], keys["k3"], page_status=st, per_page=True)
     assert (st.cpu().numpy() == 1).all()
     assert hip.device_diag() == 0
+    # the default limit encodes the same pages again, synchronously
+    hip.fused_encode_cold_pages_peak_into(e["k"], e["v"], e["th"], blobs, w.preset, w.rope_mode, w.rope_dim,
+                                          w.payload_bytes, W.TENANT_HASH, W.MODEL_HASH, 0, 0, 0, keys["k0"],
+                                          keys["k1"], keys["mk0"], keys["mk1"], keys["k2"], keys["k3"])
+    assert torch.equal(blobs, e["blobs"])
+
+
+@pytest.mark.parametrize("limit", [16, 32])
+def test_one_expired_wait_ends_the_workgroup_promptly(env, hip, limit):
+    """With a small nonzero wait limit the MAC / verify wave's first wait (the
+    first row takes tens of microseconds) expires in every workgroup; every
+    later wait of the workgroup then returns at its next poll, so each launch
+    still ends in about a normal launch time plus one bound, and fails
+    closed.  (If each later wait spun out its own bound, the hundreds of
+    waits per wave would take milliseconds.)"""
+    e = env
+    N, W, keys, w = e["N"], e["W"], e["keys"], e["w"]
+    print(f"case wait limit {limit}: egress + ingress launch times", flush=True)
+    g = N.geometry(w.num_tokens, w.num_heads, w.head_dim, w.rope_dim, N.HOT_BF16, False)
+    aad = N.Aad(W.TENANT_HASH, W.MODEL_HASH, 0, 0)
+    blobs = torch.empty_like(e["blobs"])
+    ko, vo = torch.empty_like(e["k"]), torch.empty_like(e["v"])
+    st = torch.full((N_PAGES,), -1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    s = C.c_void_p(stream.cuda_stream)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    prev = hip.debug_spin_limit(limit)
+    try:
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        rc = N.lib().ztcp_egress_peak_into_ext(
+            e["k"].data_ptr(), e["v"].data_ptr(), e["th"].data_ptr(), blobs.data_ptr(), N_PAGES, C.byref(g),
+            w.preset, w.rope_mode, w.payload_bytes, C.byref(aad), 0, C.byref(N.keys(**keys)), N.ASYNC, s)
+        assert rc == N.OK
+        ev[1].record(stream)
+        rc = N.lib().ztcp_ingress_peak_into(
+            e["blobs"].data_ptr(), e["blobs"].size(1), e["th"].data_ptr(), ko.data_ptr(), vo.data_ptr(), N_PAGES,
+            C.byref(g), W.TENANT_HASH, W.MODEL_HASH, 0, C.byref(N.keys(**keys)), st.data_ptr(),
+            N.ASYNC | N.PER_PAGE, s)
+        assert rc == N.OK
+        ev[2].record(stream)
+        torch.cuda.synchronize()
+    finally:
+        hip.debug_spin_limit(prev)
+    t_e, t_i = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    print(f"limit {limit}: egress {t_e:.3f} ms, ingress {t_i:.3f} ms", flush=True)
+    assert hip.device_diag() == 3  # both kernels' bits
+    assert not blobs[:, :16].any()
+    s_ = st.cpu().numpy()
+    assert (s_ == N.ERR_DEVICE).all()
+    assert not ko.any() and not vo.any()
+    assert t_e < 2.0 and t_i < 2.0, (t_e, t_i)
 
 
 def test_egress_extension_presets_need_the_flag(env, hip, O):
@@ -326,6 +394,13 @@ def test_argument_errors_carry_the_reference_messages(env, hip):
     ]
     for (rc, got), want_rc, msg in cases:
         assert rc == want_rc and got == msg, (rc, got, msg)
+    # two errors at once: the reference's check order decides which is reported
+    # (egress: overlap before preset, cpp:1940 / cpp:1952; ingress: the out_k
+    # overlap before the missing out_v, cpp:2283 / cpp:2288)
+    assert eg(good, preset=9, blobs=k.view(torch.uint8)) == (
+        N.EOVERLAP, "out_blobs must not alias or overlap input tensors")
+    assert ig(out_v=None, out_k=both[out.numel() - 16:out.numel() - 16 + kn], blobs=both[:out.numel()]) == (
+        N.EOVERLAP, "out_k_pages must not alias or overlap input tensors")
     with pytest.raises(RuntimeError, match="^expected_payload_bytes smaller than required payload$"):
         hip.fused_encode_cold_pages_peak_into(k, v, th, torch.zeros((2, w.blob_bytes - 4), dtype=torch.uint8,
                                                                     device="cuda"),

@@ -321,7 +321,7 @@ def test_wire_ring_egress_copy(pkg, O, W):
     print("case c2_k8v4_prefix1g: egress + wire ring pushes, no synchronization between", flush=True)
     t0 = time.perf_counter()
     P.egress(d, w.n_pages, preset=w.preset, rope_mode=w.rope_mode, expected_payload_bytes=w.payload_bytes,
-             tenant_id_hash=W.TENANT_HASH, model_id_hash=W.MODEL_HASH, **geo, **keys)
+             tenant_id_hash=W.TENANT_HASH, model_id_hash=W.MODEL_HASH, asynchronous=True, **geo, **keys)
     got = []
     for part in range(4):
         slot = ring.push(blobs[part * q:(part + 1) * q])

@@ -74,3 +74,22 @@ def test_wire_ring_partial_and_errors(hip):
     empty = ring.push(torch.zeros(0, dtype=torch.uint8, device="cuda"))
     assert ring.wait(empty).numel() == 0
     ring.close()
+
+
+def test_wire_ring_view_outlives_the_ring(hip):
+    """A view that wait() returned stays readable after the ring is closed and
+    dropped: the pinned slots are freed only with the last view."""
+    import gc
+
+    import vlx_tee_amd.serving as SV
+    ring = SV.WireRing(1 << 16, n_slots=2)
+    a = (torch.arange(1 << 16, device="cuda") * 7).to(torch.uint8)
+    view = ring.wait(ring.push(a))[100:1100]
+    ring.close()
+    del ring
+    gc.collect()
+    assert torch.equal(view, a[100:1100].cpu())
+    with pytest.raises(RuntimeError, match="closed"):
+        r2 = SV.WireRing(64, n_slots=1)
+        r2.close()
+        r2.push(torch.zeros(8, dtype=torch.uint8, device="cuda"))

@@ -126,3 +126,26 @@ def test_python_mirror_rejects_host_tensors(pkg):
         H.fused_encode_cold_pages_peak_into(k, k, torch.zeros(1, dtype=torch.int64),
                                             torch.zeros((1, 12336), dtype=torch.uint8), 1, 1, 64,
                                             12288, 0, 0, 0, 0, 0, 1, 2, 3, 4)
+
+
+def test_library_exports_exactly_the_declared_symbols(pkg):
+    """The product library's dynamic symbol table holds the entry points of
+    include/ztcp.h and include/ztcp_keyring.h and nothing else; the timer
+    build adds ztcp_phase_timers_read (include/ztcp_timers.h)."""
+    import shutil
+    import subprocess
+
+    import vlx_tee_amd._native as N
+
+    if shutil.which("nm") is None:
+        pytest.skip("nm (binutils) not available")
+
+    def exported(path):
+        out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True,
+                             check=True).stdout
+        return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+    declared = set(N.EXPORTS) | set(N.KEYRING_EXPORTS)
+    assert exported(N.LIB_PATH) == declared
+    if N.TIMERS_LIB_PATH.is_file():
+        assert exported(N.TIMERS_LIB_PATH) == declared | {"ztcp_phase_timers_read"}

@@ -95,3 +95,64 @@ def test_noalloc_rejects_batches_beyond_its_scratch(hip):
                                                 C.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == N.ESCRATCH
     assert "ZTCP_NOALLOC_MAX_PAGES" in N.last_error()
+
+
+def _noalloc(N, W, keys, geo, blobs, th, ko, vo, st, flags, stream):
+    return N.lib().ztcp_ingress_peak_into_noalloc(
+        blobs.data_ptr(), blobs.size(1), th.data_ptr(), ko.data_ptr(), vo.data_ptr(), ko.size(0), C.byref(geo),
+        W.TENANT_HASH, W.MODEL_HASH, 3, C.byref(N.keys(**keys)), None if st is None else st.data_ptr(), flags,
+        C.c_void_p(stream.cuda_stream))
+
+
+def test_noalloc_allocates_no_device_memory(hip):
+    """Device memory in use (hipMemGetInfo) is the same before and after
+    no-allocation calls of both kernel paths, once every tensor of the test
+    exists and the kernels' code is loaded."""
+    print("case no-alloc: device memory across calls", flush=True)
+    cases = [_case(hip, (16, 8, 128, 64), 2, 1, 300, 5, tamper=((3, 200),)),
+             _case(hip, (3, 1, 48, 16), 1, 1, 900, 6, tamper=((1, 60),))]
+    outs = [(torch.empty(c[6], dtype=torch.bfloat16, device="cuda"), torch.empty(c[6], dtype=torch.bfloat16,
+                                                                                   device="cuda")) for c in cases]
+    stream = torch.cuda.current_stream()
+    for (N, W, keys, geo, blobs, th, _), (ko, vo) in zip(cases, outs):  # warm: code objects loaded
+        assert _noalloc(N, W, keys, geo, blobs, th, ko, vo, None, 0, stream) == 3
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for rep in range(3):
+        for (N, W, keys, geo, blobs, th, _), (ko, vo) in zip(cases, outs):
+            assert _noalloc(N, W, keys, geo, blobs, th, ko, vo, None, N.PER_PAGE if rep else 0, stream) == 3
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
+
+
+def test_noalloc_asynchronous_call_replays_from_a_graph(hip):
+    """Only a ZTCP_ASYNC call can be captured: a synchronous one on a stream
+    under capture is refused with ZTCP_EINVAL, and a captured asynchronous call
+    replays correctly several times, with eager work on the same buffers and
+    synchronizations between the replays."""
+    N, W, keys, geo, blobs, th, sh = _case(hip, (16, 4, 128, 64), 1, 1, 256, 11)
+    want = _run(N, W, keys, geo, blobs, th, sh, "ztcp_ingress_peak_into", 0, True)
+    assert want[0] == 0
+    ko = torch.empty(sh, dtype=torch.bfloat16, device="cuda")
+    vo = torch.empty(sh, dtype=torch.bfloat16, device="cuda")
+    st = torch.full((sh[0],), -1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):  # warm outside the capture
+        assert _noalloc(N, W, keys, geo, blobs, th, ko, vo, st, N.ASYNC, s) == 0
+    torch.cuda.synchronize()
+    print("case no-alloc: graph capture of an asynchronous call", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        assert _noalloc(N, W, keys, geo, blobs, th, ko, vo, st, 0, s) == N.EINVAL
+        assert "ZTCP_ASYNC" in N.last_error()
+        assert _noalloc(N, W, keys, geo, blobs, th, ko, vo, st, N.ASYNC, s) == 0
+    for rep in range(3):
+        ko.fill_(5.0)
+        vo.fill_(5.0)
+        st.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert (st.cpu().numpy() == 0).all(), rep
+        assert torch.equal(ko, want[2]) and torch.equal(vo, want[3]), rep

@@ -24,7 +24,7 @@ HOT_FP16, HOT_BF16 = 0, 1
 # Every symbol include/ztcp.h declares.
 EXPORTS = (
     "ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes",
-    "ztcp_egress_peak_into", "ztcp_egress_peak_into_ext", "ztcp_egress_batch",
+    "ztcp_egress_peak_into", "ztcp_egress_peak_into_ext", "ztcp_egress_batch", "ztcp_egress_batch_ext",
     "ztcp_ingress_peak_into", "ztcp_ingress_peak_into_noalloc", "ztcp_ingress_batch",
     "ztcp_chacha20_xor", "ztcp_siphash128",
     "ztcp_selftest", "ztcp_device_diag", "ztcp_debug_spin_limit", "ztcp_strerror",
@@ -110,8 +110,10 @@ def lib() -> C.CDLL:
     L.ztcp_egress_peak_into.restype = i32
     L.ztcp_egress_peak_into_ext.argtypes = [P, P, P, P, i64, G, i64, i64, i64, A, u64, K, u32, P]
     L.ztcp_egress_peak_into_ext.restype = i32
-    L.ztcp_egress_batch.argtypes = [P, i64, G, i64, i64, i64, u32, u32, K, u32, P]
+    L.ztcp_egress_batch.argtypes = [P, i64, G, i64, i64, i64, u32, u32, K, P]
     L.ztcp_egress_batch.restype = i32
+    L.ztcp_egress_batch_ext.argtypes = [P, i64, G, i64, i64, i64, u32, u32, K, u32, P]
+    L.ztcp_egress_batch_ext.restype = i32
     L.ztcp_ingress_peak_into.argtypes = [P, i64, P, P, P, i64, G, u32, u32, u16, K, P, u32, P]
     L.ztcp_ingress_peak_into.restype = i32
     L.ztcp_ingress_peak_into_noalloc.argtypes = [P, i64, P, P, P, i64, G, u32, u32, u16, K, P, u32, P]

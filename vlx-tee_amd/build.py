@@ -5,7 +5,9 @@ and ``csrc/*.cpp`` (host code: the session key ring) with hipcc, one object
 per source in parallel, and links them into ``vlx-tee_amd/libztcp_hip.so``
 (exported symbols: include/ztcp.h and include/ztcp_keyring.h).
 
-It also builds ``libztcp_hip_timers.so``: the same sources with
+It also builds ``ztcp_capi_example`` (example/ztcp_capi_example.cpp, a C++
+program that calls the C ABI of include/ztcp.h through the library, as a
+serving stack would) and ``libztcp_hip_timers.so``: the same sources with
 ``-DZTCP_PHASE_TIMERS``, whose fused kernels record per-phase shader-clock
 counts (start-up, waits of each wave role, end) into a device buffer that
 ``ztcp_phase_timers_read`` returns.  Only ``bench.py --phase-timers`` loads
@@ -24,6 +26,8 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "libztcp_hip.so"
+EXAMPLE_SRC = HERE / "example" / "ztcp_capi_example.cpp"
+EXAMPLE = HERE / "ztcp_capi_example"   # a C++ caller of include/ztcp.h, linked against LIB
 LIB_TIMERS = HERE / "libztcp_hip_timers.so"
 OBJ = HERE / "_build"
 ARCH = os.environ.get("ZTCP_OFFLOAD_ARCH", "gfx950")
@@ -32,7 +36,7 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-function",
+    "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
 ]
 
 
@@ -64,7 +68,8 @@ def _build_variant(hipcc: str, out: Path, variant: str, defines: list[str], verb
 
 def _link(hipcc: str, objs: list[Path], out: Path, verbose: bool) -> None:
     tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
+           f"-Wl,--version-script={HERE / 'exports.map'}", "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd))
     subprocess.run(cmd, check=True)
@@ -84,7 +89,18 @@ def build(verbose: bool = False, timers: bool = True) -> Path:
             for f in futs:
                 f.result()
             _link(hipcc, objs, out, verbose)
+    _build_example(hipcc, verbose)
     return LIB
+
+
+def _build_example(hipcc: str, verbose: bool) -> None:
+    tmp = EXAMPLE.with_suffix(".tmp")
+    cmd = [hipcc, "-O2", "-std=c++17", "-Wall", str(EXAMPLE_SRC), "-o", str(tmp), f"-L{HERE}", "-lztcp_hip",
+           "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd))
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, EXAMPLE)
 
 
 if __name__ == "__main__":

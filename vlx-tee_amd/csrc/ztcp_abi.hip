@@ -34,8 +34,10 @@ struct DeviceCtx {
     hipEvent_t done[kCallSlots] = {};
     bool busy[kCallSlots] = {};        // taken by a call
     bool pending[kCallSlots] = {};     // released by an asynchronous call: free once done[k] completes
+    bool poisoned[kCallSlots] = {};    // lost to a failed release (its stream may still write it)
     int next = 0;
     int cu_count = 0;
+    uint32_t egress_tag = 15;          // last egress call tag (WaitSink::call_tag), 16 and up
 };
 
 std::mutex g_mu;                       // guards g_ctx and every DeviceCtx's slot bookkeeping
@@ -79,15 +81,20 @@ int device_ctx(DeviceCtx** out) {
 // released by an asynchronous call whose event has completed.  A slot held by
 // a call still in progress is never handed out (its event is stale then).
 // When every slot is taken, waits for an asynchronous call to complete, or,
-// when synchronous calls in progress hold them all, for one of those to end.
+// when synchronous calls in progress hold them all, for one of those to end;
+// when every slot is lost to failed releases, returns ZTCP_EHIP.
 int acquire_call(DeviceCtx* c, int* slot) {
     std::unique_lock<std::mutex> lock(g_mu);
     for (;;) {
-        int wait_on = -1;
+        int wait_on = -1, held = 0;
         for (int i = 0; i < kCallSlots; ++i) {
             const int k = (c->next + i) % kCallSlots;
+            if (c->poisoned[k]) continue;
             if (c->busy[k]) {
-                if (!c->pending[k]) continue;  // a call still holds it
+                if (!c->pending[k]) {  // a call still holds it
+                    ++held;
+                    continue;
+                }
                 const hipError_t q = hipEventQuery(c->done[k]);
                 if (q == hipErrorNotReady) {
                     if (wait_on < 0) wait_on = k;
@@ -101,6 +108,7 @@ int acquire_call(DeviceCtx* c, int* slot) {
             *slot = k;
             return ZTCP_OK;
         }
+        if (wait_on < 0 && held == 0) return fail_arg(ZTCP_EHIP, "every call slot of the device is lost to failed releases");
         lock.unlock();
         if (wait_on >= 0) {
             if (hipEventSynchronize(c->done[wait_on]) != hipSuccess) return ZTCP_EHIP;
@@ -120,9 +128,13 @@ int release_call(DeviceCtx* c, int slot, hipStream_t stream, bool async) {
             c->pending[slot] = true;
             return ZTCP_OK;
         }
-        // the event did not record: keep the slot out of use rather than
-        // hand it to another call while this one may still write it
-        return ZTCP_EHIP;
+        // The event did not record: wait for the stream instead.  If that
+        // fails too, the slot's kernels may still write it: it stays out of
+        // use for good (acquire_call skips it and fails once all are lost).
+        if (hipStreamSynchronize(stream) != hipSuccess) {
+            c->poisoned[slot] = true;
+            return ZTCP_EHIP;
+        }
     }
     c->busy[slot] = false;
     c->pending[slot] = false;
@@ -199,25 +211,13 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
                   int64_t preset, int64_t rope_mode, int64_t expected_payload, const ztcp_aad* aad,
                   uint64_t base_seq, const ztcp_keys* keys, uint32_t flags, hipStream_t stream) {
     t_last_error = "";
+    // the reference's order (cpp:1934-1957): dimensions, overlaps, preset and
+    // RoPE mode, payload size
     int rc = check_geometry(g, batch, "Invalid k_pages dimensions");
     if (rc) return rc;
     if (!aad || !keys) return fail_arg(ZTCP_EINVAL, "aad and keys must not be NULL");
-    // cpp:1947-1948; the extension presets only when the call asks for them
-    const bool ext = (flags & ZTCP_EXT_LAYOUTS) != 0;
-    if (preset < 1 || preset > (ext ? 6 : 3))
-        return fail_arg(ZTCP_EINVAL, ext ? "Invalid preset (must be 1..6)" : "Invalid preset (must be 1..3)");
-    if (rope_mode < 0 || rope_mode > (ext ? 3 : 2))
-        return fail_arg(ZTCP_EINVAL, ext ? "Invalid rope_mode (must be 0..3)" : "Invalid rope_mode (must be 0..2)");
-    const int64_t vecs = g->num_tokens * g->num_heads;
-    const bool has_v = descs ? !g->is_mla_single_buffer : (v != nullptr);
-    Layout lay;
-    if (!build_layout(preset, rope_mode, vecs, g->head_dim, g->rope_dim, has_v, lay))
-        return fail_arg(ZTCP_EINVAL, "head_dim / rope_dim not divisible by the extension preset's group size");
-    if (expected_payload < (int64_t)lay.required)
-        return fail_arg(ZTCP_EINVAL, "expected_payload_bytes smaller than required payload");  // cpp:1955-1957
-    if (expected_payload > ((int64_t)1 << 31))
-        return fail_arg(ZTCP_EINVAL, "expected_payload_bytes too large (at most 2^31)");
     const int64_t blob_bytes = kHeader + expected_payload + kTag;
+    const int64_t vecs = g->num_tokens * g->num_heads;
     const int64_t page_bytes = vecs * g->head_dim * 2;
     if (!descs) {
         if (!k || !blobs) return fail_arg(ZTCP_EINVAL, "k_pages and out_blobs must not be NULL");
@@ -228,6 +228,20 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
         if (overlap(blobs, out_n, v, page_bytes * batch))
             return fail_arg(ZTCP_EOVERLAP, "out_blobs must not alias or overlap v_pages");
     }
+    // cpp:1952-1953; the extension presets only when the call asks for them
+    const bool ext = (flags & ZTCP_EXT_LAYOUTS) != 0;
+    if (preset < 1 || preset > (ext ? 6 : 3))
+        return fail_arg(ZTCP_EINVAL, ext ? "Invalid preset (must be 1..6)" : "Invalid preset (must be 1..3)");
+    if (rope_mode < 0 || rope_mode > (ext ? 3 : 2))
+        return fail_arg(ZTCP_EINVAL, ext ? "Invalid rope_mode (must be 0..3)" : "Invalid rope_mode (must be 0..2)");
+    const bool has_v = descs ? !g->is_mla_single_buffer : (v != nullptr);
+    Layout lay;
+    if (!build_layout(preset, rope_mode, vecs, g->head_dim, g->rope_dim, has_v, lay))
+        return fail_arg(ZTCP_EINVAL, "head_dim / rope_dim not divisible by the extension preset's group size");
+    if (expected_payload < (int64_t)lay.required)
+        return fail_arg(ZTCP_EINVAL, "expected_payload_bytes smaller than required payload");  // cpp:1955-1957
+    if (expected_payload > ((int64_t)1 << 31))
+        return fail_arg(ZTCP_EINVAL, "expected_payload_bytes too large (at most 2^31)");
     DeviceCtx* ctx = nullptr;
     rc = device_ctx(&ctx);
     if (rc) return rc;
@@ -256,14 +270,43 @@ int egress_common(const void* k, const void* v, const int64_t* tok, uint8_t* blo
     p.nonce2 = ((uint32_t)aad->layer_id << 16) | (uint32_t)aad->head_group_id;  // cpp:108-109
     p.base_seq = base_seq;
     p.ppw = pages_per_group(batch, ctx->cu_count);
-    p.sink = wait_sink(ctx, nullptr);
 
     const bool fast = lay.aligned && expected_payload == (int64_t)lay.required && blob_bytes % 16 == 0 &&
                       (descs || (aligned16(k) && aligned16(v) && aligned16(blobs)));
-    if (fast) p.timers = timer_record(0, (batch + p.ppw - 1) / p.ppw);
-    hipError_t e = fast ? launch_egress_fused(p, g->hot_dtype, stream)
-                        : launch_egress_generic(p, g->hot_dtype, stream);
-    return e == hipSuccess ? ZTCP_OK : ZTCP_EHIP;
+    const bool async = (flags & ZTCP_ASYNC) != 0;
+    if (!fast) {  // the generic kernels have no hand-offs, hence no bounded waits
+        p.sink = wait_sink(ctx, nullptr);
+        const hipError_t e = launch_egress_generic(p, g->hot_dtype, stream);
+        if (e == hipSuccess && !async && hipStreamSynchronize(stream) != hipSuccess) return ZTCP_EHIP;
+        return e == hipSuccess ? ZTCP_OK : ZTCP_EHIP;
+    }
+    // The fused kernel reports an expired bounded wait into this call's slot,
+    // raising its diag word to the call's tag (no reset kernel needed).
+    int slot = 0;
+    rc = acquire_call(ctx, &slot);
+    if (rc) return rc;
+    CallState* call = ctx->calls + slot;
+    uint32_t tag;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        tag = ctx->egress_tag = ctx->egress_tag == 0xFFFFFFFFu ? 16u : ctx->egress_tag + 1u;
+    }
+    p.sink = wait_sink(ctx, call);
+    p.sink.call_tag = tag;
+    p.timers = timer_record(0, (batch + p.ppw - 1) / p.ppw);
+    hipError_t e = launch_egress_fused(p, g->hot_dtype, stream);
+    if (e == hipSuccess && !async) e = hipMemcpyAsync(ctx->host_calls + slot, call, sizeof(CallState),
+                                                      hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess && !async) e = hipStreamSynchronize(stream);
+    const bool expired = e == hipSuccess && !async && ctx->host_calls[slot].diag == tag;
+    if (expired) {  // fail closed: every blob of the call is zeroed before the call returns
+        e = launch_egress_zero_blobs(p, stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    }
+    const int rel = release_call(ctx, slot, stream, async || e != hipSuccess);
+    if (e != hipSuccess) return ZTCP_EHIP;
+    if (rel) return rel;
+    return expired ? ZTCP_EDEVICE : ZTCP_OK;
 }
 
 // An ingress call's validated parameters: the reference's argument checks
@@ -293,10 +336,10 @@ int ingress_prepare(const uint8_t* blobs, int64_t blob_bytes, const int64_t* tok
     if (!descs) {
         if (!blobs || !out_k) return fail_arg(ZTCP_EINVAL, "cold_blobs and out_k_pages must not be NULL");
         if (!tok) return fail_arg(ZTCP_EINVAL, "expected_token_hashes must not be NULL");
-        if (!mla && !out_v) return fail_arg(ZTCP_EINVAL, "out_v_pages is required for non-MLA geometry");  // cpp:2288
         const int64_t kn = page_bytes * batch, bn = blob_bytes * batch;
         if (overlap(out_k, kn, blobs, bn) || overlap(out_k, kn, tok, 8 * batch))  // cpp:2283
             return fail_arg(ZTCP_EOVERLAP, "out_k_pages must not alias or overlap input tensors");
+        if (!mla && !out_v) return fail_arg(ZTCP_EINVAL, "out_v_pages is required for non-MLA geometry");  // cpp:2288
         if (!mla && overlap(out_k, kn, out_v, kn))  // cpp:2292
             return fail_arg(ZTCP_EOVERLAP, "out_k_pages and out_v_pages must not alias or overlap in memory");
         if (!mla && (overlap(out_v, kn, blobs, bn) || overlap(out_v, kn, tok, 8 * batch)))  // cpp:2293-2294
@@ -495,14 +538,22 @@ int ztcp_egress_peak_into(const void* k_pages, const void* v_pages, const int64_
                                      expected_payload_bytes, aad, base_sequence_nonce, keys, 0u, stream);
 }
 
-int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages, const ztcp_geometry* g,
-                      int64_t preset, int64_t rope_mode, int64_t expected_payload_bytes,
-                      uint32_t tenant_id_hash, uint32_t model_id_hash, const ztcp_keys* keys,
-                      uint32_t flags, void* stream) {
+int ztcp_egress_batch_ext(const ztcp_page_desc* pages, int64_t n_pages, const ztcp_geometry* g,
+                          int64_t preset, int64_t rope_mode, int64_t expected_payload_bytes,
+                          uint32_t tenant_id_hash, uint32_t model_id_hash, const ztcp_keys* keys,
+                          uint32_t flags, void* stream) {
     if (!pages) return fail_arg(ZTCP_EINVAL, "pages must not be NULL");
     const ztcp_aad aad{tenant_id_hash, model_id_hash, 0, 0};  // layer / head group per page
     return egress_common(nullptr, nullptr, nullptr, nullptr, pages, n_pages, g, preset, rope_mode,
                          expected_payload_bytes, &aad, 0, keys, flags, (hipStream_t)stream);
+}
+
+int ztcp_egress_batch(const ztcp_page_desc* pages, int64_t n_pages, const ztcp_geometry* g,
+                      int64_t preset, int64_t rope_mode, int64_t expected_payload_bytes,
+                      uint32_t tenant_id_hash, uint32_t model_id_hash, const ztcp_keys* keys,
+                      void* stream) {
+    return ztcp_egress_batch_ext(pages, n_pages, g, preset, rope_mode, expected_payload_bytes, tenant_id_hash,
+                                 model_id_hash, keys, 0u, stream);
 }
 
 int ztcp_ingress_peak_into(const uint8_t* cold_blobs, int64_t blob_bytes,
@@ -531,6 +582,12 @@ int ztcp_ingress_peak_into_noalloc(const uint8_t* cold_blobs, int64_t blob_bytes
                                    const ztcp_keys* keys, int32_t* page_status, uint32_t flags, void* stream) {
     if (batch > kNoAllocPages)
         return fail_arg(ZTCP_ESCRATCH, "batch exceeds ZTCP_NOALLOC_MAX_PAGES (the no-allocation scratch capacity)");
+    // a synchronous call copies its verdict to the host and waits for the
+    // stream, neither of which a stream under capture allows
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess) return ZTCP_EHIP;
+    if (cap != hipStreamCaptureStatusNone && !(flags & ZTCP_ASYNC))
+        return fail_arg(ZTCP_EINVAL, "a stream under capture needs ZTCP_ASYNC (verdicts in page_status)");
     IngressCall c;
     int rc = ingress_prepare(cold_blobs, blob_bytes, expected_token_hashes, out_k_pages, out_v_pages, nullptr, batch,
                              g, expected_tenant_hash, expected_model_hash, expected_layer_id, keys, page_status,
@@ -589,15 +646,17 @@ int ztcp_selftest(void) {
 }
 
 int ztcp_device_diag(void) {
-    DeviceCtx* ctx = nullptr;
-    int rc = device_ctx(&ctx);
-    if (rc) return rc;
-    if (hipDeviceSynchronize() != hipSuccess) return ZTCP_EHIP;
-    // the library's sticky word, and the no-allocation path's when that path
-    // has been used on this device
-    uint32_t* words[2] = {&ctx->state->diag, nullptr};
+    // the library's sticky word when the allocating entry points have set up
+    // this device, and the no-allocation path's when that path has: reading
+    // them allocates nothing
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return ZTCP_EHIP;
+    if (hipDeviceSynchronize() != hipSuccess) return ZTCP_EHIP;
+    uint32_t* words[2] = {nullptr, nullptr};
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        if (dev < (int)g_ctx.size() && g_ctx[dev]) words[0] = &g_ctx[dev]->state->diag;
+    }
     {
         std::lock_guard<std::mutex> lock(g_noalloc_mu);
         if (dev < kMaxDevices && g_noalloc[dev].scratch)

@@ -740,7 +740,22 @@ __global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(
 
 }  // namespace
 
+// Zeroes every blob of a call (a synchronous egress whose bounded wait
+// expired: fail closed, as the reference's wrapper zeroes out_blobs on any
+// failure, nfc:597-600).  One workgroup per page, 16 bytes per thread.
+__global__ void egress_zero_blobs_kernel(EgressParams p) {
+    uint8_t* blob = egress_page(p, (int64_t)blockIdx.x).blob;
+    for (uint32_t i = threadIdx.x; i < p.blob_bytes / 16u; i += blockDim.x) stg16(blob, i, make_uint4(0u, 0u, 0u, 0u));
+    for (uint32_t i = (p.blob_bytes & ~15u) + threadIdx.x; i < p.blob_bytes; i += blockDim.x) blob[i] = 0;
+}
+
 size_t egress_fused_lds_bytes() { return (size_t)kLdsWords * sizeof(uint32_t); }
+
+hipError_t launch_egress_zero_blobs(const EgressParams& p, hipStream_t s) {
+    if (p.batch > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(egress_zero_blobs_kernel, dim3((uint32_t)p.batch), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
 
 hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) {
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;

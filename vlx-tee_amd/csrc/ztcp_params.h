@@ -34,11 +34,16 @@ struct CallState {
     uint32_t pad;
 };
 
-// What a bounded wait reports to when it expires.
+// What a bounded wait reports to when it expires.  Ingress or-s its kDiag*
+// bit into the call's diag word (reset by the call's first kernel); egress
+// raises it to the call's tag instead (atomic max of a per-device call
+// counter, never below 16), so the host learns of an expiry in this call
+// without a reset kernel: the word equals the tag only if this call wrote it.
 struct WaitSink {
     uint32_t* dev_diag;        // DeviceState::diag (sticky, per device)
-    uint32_t* call_diag;       // CallState::diag, or nullptr (egress)
+    uint32_t* call_diag;       // CallState::diag, or nullptr
     uint32_t spin_limit;       // polls before giving up
+    uint32_t call_tag;         // 0: or the kDiag* bit into call_diag; else max it with this tag
 };
 
 struct EgressParams {
@@ -182,6 +187,7 @@ __device__ __forceinline__ GroupCursor group_cursor(int32_t G0, int32_t gpv, int
 hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s);
 hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s);
 hipError_t launch_egress_generic(const EgressParams& p, int dtype, hipStream_t s);
+hipError_t launch_egress_zero_blobs(const EgressParams& p, hipStream_t s);
 hipError_t launch_ingress_generic_impl(const IngressParams& p, int dtype, int32_t* status,
                                        hipStream_t s);
 hipError_t launch_ingress_finalize(const IngressParams& p, hipStream_t s);

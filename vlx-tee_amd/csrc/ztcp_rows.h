@@ -151,13 +151,14 @@ struct Waiter {
     uint32_t* call_diag;   // nullptr: no per-call record
     uint32_t* expired;     // LDS
     uint32_t spin_limit;
+    uint32_t call_tag;     // WaitSink::call_tag
     uint32_t* tm;          // LDS phase-timer counters (timer builds)
     uint64_t t0;           // clock at which the wave left the first barrier (timer builds)
 };
 
 __device__ __forceinline__ Waiter make_waiter(const WaitSink& s, uint32_t* expired_lds, uint32_t* tm = nullptr,
                                               uint64_t t0 = 0) {
-    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit, tm, t0};
+    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit, s.call_tag, tm, t0};
 }
 
 // Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
@@ -178,7 +179,10 @@ __device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, cons
         if (spin >= w.spin_limit) {
             if ((threadIdx.x & 63) == 0) {
                 atomicOr(w.dev_diag, DIAG);
-                if (w.call_diag) atomicOr(w.call_diag, DIAG);
+                if (w.call_diag) {
+                    if (w.call_tag) atomicMax(w.call_diag, w.call_tag);
+                    else atomicOr(w.call_diag, DIAG);
+                }
             }
             __hip_atomic_store(w.expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             break;

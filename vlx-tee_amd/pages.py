@@ -52,16 +52,21 @@ def egress(descs: torch.Tensor, n_pages: int, *, num_tokens: int, num_heads: int
            rope_dim: int, dtype: torch.dtype, is_mla_single_buffer: bool, preset: int,
            rope_mode: int, expected_payload_bytes: int, tenant_id_hash: int, model_id_hash: int,
            k0: int, k1: int, mk0: int, mk1: int, k2: int = 0, k3: int = 0,
-           ext_layouts: bool = False) -> None:
-    """``ext_layouts`` admits the extension presets 4..6 / RoPE mode 3."""
+           ext_layouts: bool = False, asynchronous: bool = False) -> None:
+    """``ext_layouts`` admits the extension presets 4..6 / RoPE mode 3.
+    Synchronous unless ``asynchronous``: an expired device-side wait then
+    raises (every blob zeroed); asynchronously it shows as blobs no ingress
+    accepts and in ``native_hip_codec.device_diag()``."""
     g = N.geometry(num_tokens, num_heads, head_dim, rope_dim, _DTYPES[dtype], is_mla_single_buffer)
-    rc = N.lib().ztcp_egress_batch(descs.data_ptr(), n_pages, C.byref(g), preset, rope_mode,
-                                   expected_payload_bytes, tenant_id_hash & 0xFFFFFFFF,
-                                   model_id_hash & 0xFFFFFFFF,
-                                   C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)),
-                                   N.EXT_LAYOUTS if ext_layouts else 0, _stream())
+    flags = (N.EXT_LAYOUTS if ext_layouts else 0) | (N.ASYNC if asynchronous else 0)
+    rc = N.lib().ztcp_egress_batch_ext(descs.data_ptr(), n_pages, C.byref(g), preset, rope_mode,
+                                       expected_payload_bytes, tenant_id_hash & 0xFFFFFFFF,
+                                       model_id_hash & 0xFFFFFFFF,
+                                       C.byref(N.keys(k0, k1, mk0, mk1, k2, k3)), flags, _stream())
     if rc in (N.EINVAL, N.EOVERLAP):
         raise RuntimeError(f"ztcp_egress_batch: {N.last_error()}")
+    if rc == N.EDEVICE:
+        raise RuntimeError("KV_INTEGRITY_ERROR: device-side bounded wait expired; outputs zeroed")
     if rc != N.OK:
         raise RuntimeError(f"ztcp_egress_batch: {N.strerror(rc)} ({rc})")
 

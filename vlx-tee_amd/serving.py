@@ -58,6 +58,35 @@ def hit_bitmap(page_status: torch.Tensor, packed: bool = False) -> torch.Tensor:
     return out
 
 
+class _RingHandle:
+    """Owns a native ring (ztcp_wire_ring_*): destroyed when the last of its
+    holders is gone -- the WireRing and every host view that ``wait``
+    returned, since those views are the ring's pinned slot memory."""
+
+    def __init__(self, ptr: C.c_void_p, destroy=None):
+        self.ptr = ptr
+        self._destroy = destroy if destroy is not None else (lambda p: N.lib().ztcp_wire_ring_destroy(p))
+
+    def __del__(self):
+        if self.ptr:
+            ptr, self.ptr = self.ptr, None
+            try:
+                self._destroy(ptr)
+            except Exception:  # noqa: BLE001  (interpreter shutdown)
+                pass
+
+
+def _host_view(address: int, nbytes: int, owner) -> torch.Tensor:
+    """A uint8 host tensor over ``nbytes`` at ``address`` that keeps ``owner``
+    (the memory's holder) alive for as long as the tensor or any view of it
+    exists: tensor -> numpy array -> memoryview -> ctypes array -> owner."""
+    if nbytes == 0:
+        return torch.empty(0, dtype=torch.uint8)
+    buf = (C.c_uint8 * nbytes).from_address(address)
+    buf._owner = owner
+    return torch.from_numpy(np.ctypeslib.as_array(buf))
+
+
 class WireRing:
     """A ring of ``n_slots`` pinned host buffers of ``slot_bytes`` each, with a
     copy stream of its own (the library's ztcp_wire_ring).
@@ -68,7 +97,9 @@ class WireRing:
     ``wait(slot)`` blocks until that copy has landed and returns the slot's
     bytes as a host tensor (a view of the pinned slot).  A slot is reused
     ``n_slots`` pushes later, after its previous copy has landed, so the bytes
-    ``wait`` returned stay valid until then."""
+    ``wait`` returned stay those of that push until then.  The views keep the
+    ring's memory alive: ``close()`` (or dropping the ring) frees it only once
+    no view that ``wait`` returned is left."""
 
     def __init__(self, slot_bytes: int, n_slots: int = 2, device: torch.device | int | None = None):
         if slot_bytes <= 0 or n_slots <= 0:
@@ -78,11 +109,17 @@ class WireRing:
         self.slot_bytes = slot_bytes
         self.device = torch.device("cuda", torch.cuda.current_device() if device is None else
                                    torch.device(device).index or 0)
-        self._ring = C.c_void_p()
+        ring = C.c_void_p()
         with torch.cuda.device(self.device):
-            rc = N.lib().ztcp_wire_ring_create(slot_bytes, n_slots, C.byref(self._ring))
+            rc = N.lib().ztcp_wire_ring_create(slot_bytes, n_slots, C.byref(ring))
         _raise(rc, "ztcp_wire_ring_create")
+        self._h: _RingHandle | None = _RingHandle(ring)
         self._held: dict[int, torch.Tensor] = {}  # slot -> device blobs still being copied
+
+    def _ptr(self) -> C.c_void_p:
+        if self._h is None:
+            raise RuntimeError("WireRing is closed")
+        return self._h.ptr
 
     def push(self, blobs: torch.Tensor) -> int:
         if blobs.device != self.device or blobs.dtype != torch.uint8 or not blobs.is_contiguous():
@@ -92,7 +129,7 @@ class WireRing:
             raise ValueError(f"{n} blob bytes exceed the slot size {self.slot_bytes}")
         slot = C.c_int32(-1)
         with torch.cuda.device(self.device):
-            rc = N.lib().ztcp_wire_ring_push(self._ring, C.c_void_p(blobs.data_ptr()), n,
+            rc = N.lib().ztcp_wire_ring_push(self._ptr(), C.c_void_p(blobs.data_ptr()), n,
                                              _stream(self.device), C.byref(slot))
         _raise(rc, "ztcp_wire_ring_push")
         self._held[slot.value] = blobs  # the copy reads it on the ring's stream
@@ -100,25 +137,19 @@ class WireRing:
 
     def wait(self, slot: int) -> torch.Tensor:
         host, n = C.c_void_p(), C.c_size_t()
-        rc = N.lib().ztcp_wire_ring_wait(self._ring, slot, C.byref(host), C.byref(n))
+        rc = N.lib().ztcp_wire_ring_wait(self._ptr(), slot, C.byref(host), C.byref(n))
         if rc == N.EINVAL:
             raise ValueError(f"slot {slot} holds no copy")
         _raise(rc, "ztcp_wire_ring_wait")
         self._held.pop(slot, None)
-        if n.value == 0:
-            return torch.empty(0, dtype=torch.uint8)
-        buf = (C.c_uint8 * n.value).from_address(host.value)
-        return torch.from_numpy(np.ctypeslib.as_array(buf))
+        return _host_view(host.value or 0, n.value, self._h)
 
     def close(self) -> None:
-        if self._ring:
-            rc = N.lib().ztcp_wire_ring_destroy(self._ring)
-            self._ring = C.c_void_p()
-            self._held.clear()
-            _raise(rc, "ztcp_wire_ring_destroy")
+        """Releases the ring; its memory is freed once no view from ``wait``
+        is left (at once if there is none).  The copies in flight complete
+        first (ztcp_wire_ring_destroy)."""
+        self._h = None
+        self._held.clear()
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:  # noqa: BLE001
-            pass
+        self._h = None
