@@ -59,7 +59,8 @@ def _log(msg: str) -> None:
 # Phase-timer slots (TimerSlot in vlx-tee_amd/csrc/ztcp_rows.h).
 _TM = dict(mac_rows_begin=0, mac_first_row=1, mac_rows_end=2, mac_end=3, wg_end=4, prod_first_row=5,
            prod_last=6, prod_busy=7, mac_wait=8, mac_miss=16, ring_wait=24, stage_wait=25, free_wait=26,
-           storer_wait=27, feed_wait=28, storer_end=29, feed_end=30, prod_waves=31, rows=32,
+           storer_wait=27, feed_wait=28, storer_end=29, feed_end=30, prod_waves=31, rows=32, prod_setup=33,
+           prod_loaded=34,
            abs_start=40, abs_end=41, real_start=42, real_end=43)
 
 
@@ -85,7 +86,8 @@ def summarize_phase_timers(rec) -> dict:
                  wait_total=m(sum(col("mac_wait", i) for i in range(8))),
                  wait_by_64_rows=[m(col("mac_wait", i)) for i in range(8)],
                  rows_not_ready_by_64_rows=[m(col("mac_miss", i)) for i in range(8)]),
-        workers=dict(waves=m(col("prod_waves")), rows=m(col("rows")), first_row=m(col("prod_first_row")),
+        workers=dict(waves=m(col("prod_waves")), rows=m(col("rows")), setup=m(col("prod_setup")),
+                     first_data=m(col("prod_loaded")), first_row=m(col("prod_first_row")),
                      last=m(col("prod_last")), busy_per_wave=m(col("prod_busy") / waves),
                      ring_wait_per_wave=m(col("ring_wait") / waves),
                      stage_wait_per_wave=m(col("stage_wait") / waves),
@@ -208,8 +210,14 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float, timers: bool =
     phase = None
     if timers:  # the records of the last step's two launches
         import vlx_tee_amd._native as N
+        rows = w.payload_bytes // 64
         phase = dict(egress=summarize_phase_timers(N.phase_timers(0)),
                      ingress=summarize_phase_timers(N.phase_timers(1)))
+        for d, name in ((0, "egress"), (1, "ingress")):
+            arrive, absorb, wait_flag, reread = N.phase_trace(d)
+            phase[name]["trace_wg0"] = dict(arrive=arrive[:rows].tolist(), absorb=absorb[:rows].tolist(),
+                                            slow_flag_wait=wait_flag[:rows].tolist(),
+                                            slow_reread=reread[:rows].tolist())
     hot = w.n_pages * w.hot_bytes_per_page
     wire = w.n_pages * w.blob_bytes
     me, mi = statistics.mean(te), statistics.mean(ti)
@@ -544,7 +552,7 @@ def main() -> None:
             r = run_gpu(wn, a.steps, a.warmup, a.settle_seconds, timers=True)
             out[wn] = dict(egress_ms=round(r["egress_ms"], 4), ingress_ms=round(r["ingress_ms"], 4),
                            phase_timers=r["phase_timers"])
-            _log(f"{wn}: {json.dumps(out[wn])}")
+            _log(f"{wn}: egress {out[wn]['egress_ms']} ms, ingress {out[wn]['ingress_ms']} ms")
         print(json.dumps(dict(phase_timers=out, build="libztcp_hip_timers.so")))
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

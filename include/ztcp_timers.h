@@ -33,6 +33,7 @@ extern "C" {
 
 #define ZTCP_TIMER_SLOTS 48
 #define ZTCP_TIMER_MAX_WORKGROUPS 4096
+#define ZTCP_TRACE_ROWS 1024
 
 /* Copies the records of the last fused launch of `direction` (0 = egress,
  * 1 = ingress) on the current device into `out` (HOST, max_words words),
@@ -40,6 +41,17 @@ extern "C" {
  * (workgroups * ZTCP_TIMER_SLOTS), 0 when no fused launch was recorded, or a
  * negative ZTCP_E* code. */
 ZTCP_API int64_t ztcp_phase_timers_read(int32_t direction, uint64_t* out, int64_t max_words);
+
+/* Workgroup 0's row trace of the same launch: 4 * ZTCP_TRACE_ROWS 32-bit
+ * words.  Clocks since its first barrier: out[r] when payload row r reached
+ * the ring, out[ZTCP_TRACE_ROWS + r] when the MAC / verify wave absorbed it;
+ * for a row whose ready flag that wave found unset when it fetched the row,
+ * the clocks it then waited for the flag (out[2 * ZTCP_TRACE_ROWS + r]) and
+ * for the re-read of the row's data (out[3 * ZTCP_TRACE_ROWS + r]); rows
+ * past the payload, and the last two words of fast-path rows, keep whatever
+ * an earlier launch left there.  Returns 4 * ZTCP_TRACE_ROWS, 0 when no fused
+ * launch was recorded, or a negative ZTCP_E* code. */
+ZTCP_API int64_t ztcp_phase_trace_read(int32_t direction, uint32_t* out, int64_t max_words);
 
 #ifdef __cplusplus
 }

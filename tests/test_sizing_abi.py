@@ -148,4 +148,4 @@ def test_library_exports_exactly_the_declared_symbols(pkg):
     declared = set(N.EXPORTS) | set(N.KEYRING_EXPORTS)
     assert exported(N.LIB_PATH) == declared
     if N.TIMERS_LIB_PATH.is_file():
-        assert exported(N.TIMERS_LIB_PATH) == declared | {"ztcp_phase_timers_read"}
+        assert exported(N.TIMERS_LIB_PATH) == declared | {"ztcp_phase_timers_read", "ztcp_phase_trace_read"}

@@ -100,6 +100,8 @@ def lib() -> C.CDLL:
     if LIB_PATH == TIMERS_LIB_PATH:
         L.ztcp_phase_timers_read.argtypes = [C.c_int32, C.c_void_p, C.c_int64]
         L.ztcp_phase_timers_read.restype = C.c_int64
+        L.ztcp_phase_trace_read.argtypes = [C.c_int32, C.c_void_p, C.c_int64]
+        L.ztcp_phase_trace_read.restype = C.c_int64
     P, G, A, K = C.c_void_p, C.POINTER(Geometry), C.POINTER(Aad), C.POINTER(Keys)
     i64, u64, u32, u16, i32 = C.c_int64, C.c_uint64, C.c_uint32, C.c_uint16, C.c_int
     for name in ("ztcp_payload_bytes", "ztcp_required_payload_bytes", "ztcp_blob_bytes"):
@@ -182,6 +184,7 @@ def _bind_keyring(L: C.CDLL) -> None:
 
 
 TIMER_SLOTS = 48  # include/ztcp_timers.h ZTCP_TIMER_SLOTS
+TRACE_ROWS = 1024  # ZTCP_TRACE_ROWS
 
 
 def phase_timers(direction: int):
@@ -197,6 +200,20 @@ def phase_timers(direction: int):
     if n < 0:
         raise RuntimeError(f"ztcp_phase_timers_read: {strerror(int(n))}")
     return buf[:n].reshape(-1, TIMER_SLOTS)
+
+
+def phase_trace(direction: int):
+    """Workgroup 0's row trace of the last fused launch of `direction`:
+    uint32 arrays of TRACE_ROWS (ring arrival clocks, absorption clocks,
+    slow-path flag wait, slow-path re-read)."""
+    import numpy as np
+
+    L = lib()
+    buf = np.zeros(4 * TRACE_ROWS, dtype=np.uint32)
+    n = L.ztcp_phase_trace_read(direction, buf.ctypes.data, buf.size)
+    if n < 0:
+        raise RuntimeError(f"ztcp_phase_trace_read: {strerror(int(n))}")
+    return tuple(buf[i * TRACE_ROWS:(i + 1) * TRACE_ROWS] for i in range(4))
 
 
 def strerror(code: int) -> str:

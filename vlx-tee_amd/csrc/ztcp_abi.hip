@@ -144,15 +144,16 @@ int release_call(DeviceCtx* c, int slot, hipStream_t stream, bool async) {
 #ifdef ZTCP_PHASE_TIMERS
 // Phase-timer records of the last fused launch per direction (diagnostic
 // build only): one buffer per direction, on the device of the first launch.
-static_assert(kTimerSlots == ZTCP_TIMER_SLOTS, "timer record size");
+static_assert(kTimerSlots == ZTCP_TIMER_SLOTS && kTimerMaxWg == ZTCP_TIMER_MAX_WORKGROUPS &&
+                  kTraceRows == ZTCP_TRACE_ROWS, "timer record size");
 unsigned long long* g_timer_buf[2] = {nullptr, nullptr};
 int64_t g_timer_wgs[2] = {0, 0};
 unsigned long long* timer_record(int dir, int64_t grid) {
     std::lock_guard<std::mutex> lock(g_mu);
     if (grid > ZTCP_TIMER_MAX_WORKGROUPS) return nullptr;
     if (!g_timer_buf[dir] &&
-        hipMalloc(&g_timer_buf[dir], sizeof(unsigned long long) * kTimerSlots * ZTCP_TIMER_MAX_WORKGROUPS) !=
-            hipSuccess)
+        hipMalloc(&g_timer_buf[dir], sizeof(unsigned long long) * (kTimerSlots * ZTCP_TIMER_MAX_WORKGROUPS +
+                                                                     2 * kTraceRows)) != hipSuccess)
         return g_timer_buf[dir] = nullptr;
     g_timer_wgs[dir] = grid;
     return g_timer_buf[dir];
@@ -713,6 +714,22 @@ int64_t ztcp_phase_timers_read(int32_t direction, uint64_t* out, int64_t max_wor
     if (n > max_words) return ZTCP_EINVAL;
     if (hipMemcpy(out, buf, sizeof(uint64_t) * (size_t)n, hipMemcpyDeviceToHost) != hipSuccess) return ZTCP_EHIP;
     return n;
+}
+
+int64_t ztcp_phase_trace_read(int32_t direction, uint32_t* out, int64_t max_words) {
+    if (direction < 0 || direction > 1 || (!out && max_words > 0)) return ZTCP_EINVAL;
+    if (hipDeviceSynchronize() != hipSuccess) return ZTCP_EHIP;
+    unsigned long long* buf = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        buf = g_timer_buf[direction];
+    }
+    if (!buf) return 0;
+    if (max_words < 4 * kTraceRows) return ZTCP_EINVAL;
+    if (hipMemcpy(out, buf + (size_t)kTimerSlots * ZTCP_TIMER_MAX_WORKGROUPS, sizeof(uint32_t) * 4 * kTraceRows,
+                  hipMemcpyDeviceToHost) != hipSuccess)
+        return ZTCP_EHIP;
+    return 4 * kTraceRows;
 }
 #endif
 

@@ -421,6 +421,7 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     for (int q = 0; q < 4; ++q)
         lds_put_quad(slot, c.lane, q, make_uint4(ks[4 * q], ks[4 * q + 1], ks[4 * q + 2], ks[4 * q + 3]));
     publish(&flags[kFlagRing + row.mrow % kRing], (uint32_t)row.mrow + 1u);  // the storer wave stores it
+    tm_trace(c.wt.trace, row.mrow, c.wt.t0);
     if (nxt.valid) first_half<DT, FAM>(p, c.pg, nxt, w, pt, sc);
 }
 
@@ -436,12 +437,14 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     c.nc.init(p.key, c.n0, c.n1, c.n2);
     c.lds = lds;
     c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
+    c.wt.trace = trace_of(p.timers);
     const int32_t total = total_code_rows(p.lay);
     // The page descriptor and kernel argument loads above complete here,
     // before the loop: a load still counted as in flight where the loop
     // begins makes the compiler wait for every outstanding memory operation
     // wherever the loop uses its result.
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPhaseTimers) tm_min(c.wt.tm, kTmProdSetup, phase_clock() - c.wt.t0);
     uint32_t* flags = lds + kLdsFlags;
     // code rows are handed out in order from an LDS counter, one row ahead of
     // the one being made (so its groups can be prefetched): a slower wave
@@ -463,6 +466,7 @@ __device__ void egress_produce(const EgressParams& p, int64_t page0, int ppw, ui
     if (cur.valid) {
         load_half_any<FAM>(p, c.pg, cur, 0, w);
         first_half<DT, FAM>(p, c.pg, cur, w, pt, sc);
+        if constexpr (kPhaseTimers) tm_min(c.wt.tm, kTmProdLoaded, phase_clock() - c.wt.t0);
     }
     [[maybe_unused]] int32_t made = 0;
 #pragma unroll 1
@@ -542,7 +546,8 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     m.init(p.lay);
     // Rows arrive in MAC order in the ring (code rows from the producers,
     // scale rows from the feeder), so the next row is always the next slot.
-    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
+    Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
+    wt.trace = trace_of(p.timers);
     __builtin_amdgcn_s_waitcnt(0);
     if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsBegin, phase_clock() - t0);
     mac_rows<kRing, kDiagEgressWait>(wt, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
@@ -586,6 +591,7 @@ __device__ __forceinline__ void feed_put(const Waiter& wt, uint32_t* lds, const 
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
     publish(&flags[kFlagRing + rs % kRing], (uint32_t)rs + 1u);
+    tm_trace(wt.trace, rs, wt.t0);
 }
 
 __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
@@ -595,7 +601,8 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
     pq.init(lane);
     MacPlan m;
     m.init(p.lay);
-    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
+    Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
+    wt.trace = trace_of(p.timers);
     int32_t g0 = 0, r0 = 0;  // scale rows / MAC rows before the section
 #pragma unroll
     for (int si = 0; si < 3; ++si) {
@@ -703,6 +710,7 @@ __global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(
     const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) lds[kLdsFlags + i] = 0u;
     tm_clear(lds + kLdsTimers);
+    tm_trace_clear(p.timers);
     if (threadIdx.x < 64) {
         uint64_t* blobs = reinterpret_cast<uint64_t*>(lds + kLdsBlobs);
         blobs[threadIdx.x] = (int)threadIdx.x < ppw ? reinterpret_cast<uint64_t>(egress_page(p, page0 + threadIdx.x).blob)

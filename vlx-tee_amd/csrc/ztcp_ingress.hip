@@ -393,6 +393,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
     for (int q = 0; q < 4; ++q)
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
     publish(&flags[kFlagRing + k.mrow % kRing], (uint32_t)k.mrow + 1u);
+    tm_trace(c.wt.trace, k.mrow, c.wt.t0);
     uint32_t pt[16];
     {
         uint32_t ks[16];
@@ -480,6 +481,7 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
     for (int q = 0; q < 4; ++q)
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
     publish(&flags[kFlagRing + k.mrow % kRing], (uint32_t)k.mrow + 1u);
+    tm_trace(c.wt.trace, k.mrow, c.wt.t0);
     uint32_t pt[16];
     {
         uint32_t ks[16];
@@ -575,12 +577,14 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
     int32_t t = grab();
     Task k = task_info<FAM>(lay, t);
     uint32_t ct[16];
+    if constexpr (kPhaseTimers) tm_min(c.wt.tm, kTmProdSetup, phase_clock() - c.wt.t0);
     if (k.valid) load_block(c.pay + 64u * (uint32_t)k.block, ct);
     // The layout, descriptor and pointer-table reads complete here, before
     // the loop: a load still counted as in flight where the loop begins makes
     // the compiler wait for every outstanding memory operation wherever the
     // loop uses its result.
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPhaseTimers) tm_min(c.wt.tm, kTmProdLoaded, phase_clock() - c.wt.t0);
     [[maybe_unused]] int32_t made = 0;
 #pragma unroll 1
     while (t < total) {
@@ -632,13 +636,15 @@ __device__ __forceinline__ void feed_put(const Waiter& wt, uint32_t* lds, const 
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds_put_quad_at(slot, pq.off[q], x[q]);
     publish(&flags[kFlagRing + r % kRing], (uint32_t)r + 1u);
+    tm_trace(wt.trace, r, wt.t0);
 }
 
 __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout& lay, bool has_lay,
                              const uint8_t* pay, int lane) {
     PageQuads pq;
     pq.init(lane);
-    const Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
+    Waiter wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, phase_clock());
+    wt.trace = trace_of(p.timers);
     const int32_t total = (int32_t)(p.payload / 64u);
     // payload rows [cb_i, ce_i) are section i's code rows (decoders)
     int32_t cb[3], ce[3];
@@ -707,7 +713,8 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     s.absorb_words<4>(hdr);
     PageQuads pq;
     pq.init(lane);
-    const Waiter st = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
+    Waiter st = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
+    st.trace = trace_of(p.timers);
     __builtin_amdgcn_s_waitcnt(0);
     if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacRowsBegin, phase_clock() - t0);
     mac_rows<kRing, kDiagIngressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
@@ -751,6 +758,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     uint32_t* flags = lds + kLdsFlags;
     for (int i = threadIdx.x; i < kNumFlags; i += blockDim.x) flags[i] = 0u;
     tm_clear(lds + kLdsTimers);
+    tm_trace_clear(p.timers);
     if (threadIdx.x < 64) {
         // Pages outside the row pipeline (another layout, invalid flags) get
         // its stores too: those of another layout are decoded again below,
@@ -789,6 +797,7 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
         c.lane = lane;
         c.pq.init(lane);
         c.wt = make_waiter(p.sink, lds + kLdsFlags + kFlagExpired, lds + kLdsTimers, t0);
+        c.wt.trace = trace_of(p.timers);
         c.init_stores();
         decode_rows<DT, FAM>(c, lay);
     }

@@ -61,6 +61,8 @@ constexpr bool kPhaseTimers = true;
 constexpr bool kPhaseTimers = false;
 #endif
 constexpr int kTimerSlots = 48;        // 64-bit counters per workgroup
+constexpr int kTimerMaxWg = 4096;      // workgroups with a record
+constexpr int kTraceRows = 1024;       // rows traced in workgroup 0: [4][kTraceRows] u32 after the records
 constexpr int kTimerLdsWords = kPhaseTimers ? 2 * kTimerSlots : 0;
 enum TimerSlot : int {
     kTmMacRowsBegin = 0,   // MAC / verify wave: header absorbed, payload rows begin
@@ -82,6 +84,8 @@ enum TimerSlot : int {
     kTmFeedEnd = 30,       // feeder: done
     kTmProdWaves = 31,     // producer / decoder waves that ran
     kTmRows = 32,          // rows made by producers / decoders
+    kTmProdSetup = 33,     // earliest producer / decoder done with its page setup (descriptor, nonce cache)
+    kTmProdLoaded = 34,    // earliest producer / decoder holding its first row's data (egress: quantized)
     // written to the record by thread 0 directly
     kTmAbsStart = 40,      // s_memtime after the first barrier
     kTmAbsEnd = 41,        // s_memtime after the last barrier
@@ -120,9 +124,40 @@ __device__ __forceinline__ void tm_clear(uint32_t* tm) {
     if constexpr (kPhaseTimers) {
         if ((int)threadIdx.x < kTimerSlots)
             reinterpret_cast<unsigned long long*>(tm)[threadIdx.x] =
-                threadIdx.x == kTmProdFirstRow ? ~0ull : 0ull;
+                (threadIdx.x == kTmProdFirstRow || threadIdx.x == kTmProdSetup || threadIdx.x == kTmProdLoaded)
+                    ? ~0ull : 0ull;
     }
 }
+// Workgroup 0's row trace (timer builds): 32-bit clocks since the first
+// barrier at which each payload row reached the ring (trace[r]) and at which
+// the MAC / verify wave absorbed it (trace[kTraceRows + r]); for rows whose
+// flag the MAC / verify wave found unset when it fetched them, the clocks it
+// then waited for the flag (trace[2 kTraceRows + r]) and for the data's
+// re-read (trace[3 kTraceRows + r]).
+__device__ __forceinline__ uint32_t* trace_of(unsigned long long* timers) {
+    if constexpr (kPhaseTimers) {
+        if (timers && blockIdx.x == 0)
+            return reinterpret_cast<uint32_t*>(timers + (size_t)kTimerMaxWg * kTimerSlots);
+    }
+    return nullptr;
+}
+// Workgroup 0, every thread, before the first barrier: zero the slow-path
+// words of the trace (fast-path rows leave them 0).
+__device__ __forceinline__ void tm_trace_clear(unsigned long long* timers) {
+    if constexpr (kPhaseTimers) {
+        uint32_t* trace = trace_of(timers);
+        if (!trace) return;
+        for (int i = threadIdx.x; i < 2 * kTraceRows; i += blockDim.x) trace[2 * kTraceRows + i] = 0u;
+        __threadfence_block();
+    }
+}
+__device__ __forceinline__ void tm_trace(uint32_t* trace, int idx, uint64_t t0) {
+    if constexpr (kPhaseTimers) {
+        if (trace && idx >= 0 && idx < 4 * kTraceRows && (threadIdx.x & 63) == 0)
+            trace[idx] = (uint32_t)(phase_clock() - t0);
+    }
+}
+
 // Thread 0, after the last barrier: the LDS counters and the absolute clocks
 // into this workgroup's record (kTimerSlots words) of the call's buffer.
 __device__ __forceinline__ void tm_flush(const uint32_t* tm, unsigned long long* rec, uint64_t start,
@@ -154,11 +189,12 @@ struct Waiter {
     uint32_t call_tag;     // WaitSink::call_tag
     uint32_t* tm;          // LDS phase-timer counters (timer builds)
     uint64_t t0;           // clock at which the wave left the first barrier (timer builds)
+    uint32_t* trace;       // workgroup 0's row trace (timer builds), else nullptr
 };
 
 __device__ __forceinline__ Waiter make_waiter(const WaitSink& s, uint32_t* expired_lds, uint32_t* tm = nullptr,
                                               uint64_t t0 = 0) {
-    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit, s.call_tag, tm, t0};
+    return Waiter{s.dev_diag, s.call_diag, expired_lds, s.spin_limit, s.call_tag, tm, t0, nullptr};
 }
 
 // Waits until *flag >= want (monotonic counters; want <= 0 returns at once).
@@ -204,6 +240,17 @@ __device__ __forceinline__ void pin_words(uint32_t (&w)[16]) {
 
 __device__ __forceinline__ void publish(uint32_t* flag, uint32_t value) {
     __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// A hand-off through LDS whose data this wave read or wrote in LDS only: the
+// LDS unit performs a wave's LDS operations in issue order, so every access
+// issued before the flag store has been performed when another wave reads
+// the flag.  The empty asm keeps the compiler from moving those accesses
+// past the store; unlike a release, the store does not wait for this wave's
+// LDS reads still in flight (the MAC wave's prefetched rows).
+__device__ __forceinline__ void publish_lds(uint32_t* flag, uint32_t value) {
+    asm volatile("" ::: "memory");
+    __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // A SIMD issues the oldest of its ready waves first, so four worker waves of
@@ -259,13 +306,19 @@ __device__ __forceinline__ void mac_absorb(const Waiter& wt, const uint32_t* rin
     if (__builtin_expect(!ready, 0)) {
         [[maybe_unused]] const uint64_t t_in = phase_clock();
         wait_ge<DIAG>(ring_flags + r.slot, want, wt);
+        [[maybe_unused]] const uint64_t t_flag = phase_clock();
 #pragma unroll
         for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
         if constexpr (kPhaseTimers) {
+            const uint64_t t_out = phase_clock();
             const int b = min((want - 1) >> 6, 7);
-            tm_add(wt.tm, kTmMacWait + b, phase_clock() - t_in);
+            tm_add(wt.tm, kTmMacWait + b, t_out - t_in);
             tm_add(wt.tm, kTmMacMiss + b, 1);
+            if (wt.trace && (threadIdx.x & 63) == 0 && want <= kTraceRows) {
+                wt.trace[2 * kTraceRows + want - 1] = (uint32_t)(t_flag - t_in);
+                wt.trace[3 * kTraceRows + want - 1] = (uint32_t)(t_out - t_flag);
+            }
         }
     }
     s.absorb64_with(r.x, [&](int i) {
@@ -274,6 +327,7 @@ __device__ __forceinline__ void mac_absorb(const Waiter& wt, const uint32_t* rin
     publish(used, (uint32_t)want);
     if constexpr (kPhaseTimers) {
         if (want == 1) tm_add(wt.tm, kTmMacFirstRow, phase_clock() - wt.t0);
+        tm_trace(wt.trace, kTraceRows + want - 1, wt.t0);
     }
 }
 
