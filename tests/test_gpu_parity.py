@@ -87,10 +87,13 @@ def _verdict(err):
 
 
 GEOMS = [  # tokens, heads, head_dim, rope, mla, pages   (fast path unless noted)
+    # egress: up to 4 pages per workgroup (<= 1024 pages) run the small-batch
+    # kernel for the reference's presets, larger batches the row-pipeline one
     (16, 4, 128, 64, False, 64),     # c0 page shape
     (16, 8, 128, 64, False, 40),     # c2 page shape
     (64, 1, 576, 64, True, 6),       # c4 page shape
-    (2, 16, 32, 16, False, 700),     # several pages per workgroup
+    (2, 16, 32, 16, False, 700),     # several pages per workgroup (small-batch kernel)
+    (16, 4, 128, 64, False, 1333),   # row pipeline, 6 pages per workgroup, the last one partial
     (3, 1, 48, 32, True, 5),         # generic path (vecs % 32 != 0)
     (5, 3, 16, 16, False, 4),        # generic path
     (16, 2, 64, 0, False, 9),        # rope_dim 0

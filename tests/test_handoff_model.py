@@ -552,3 +552,86 @@ def test_one_expired_wait_ends_a_broken_ingress_workgroup():
             assert done and b.expired and 1 <= b.expiries <= 14
     finally:
         _const = real
+
+
+# ---------------------------------------------------------------------------
+# The small-batch egress kernel (egress_small_kernel): three producer waves
+# make task t = 192 k + 64 w + lane of pass k (code row t // ppw of page
+# t % ppw) and publish pass counts; after every wave's last pass they make
+# the scale rows and count themselves done.  The MAC wave reads payload rows
+# in order, a code row once every wave has published the pass that holds its
+# last page's task (need = (c ppw + ppw - 1) // 192 + 1 passes; rows below
+# need * 192 // ppw are then complete), a scale row once all three waves are
+# done.  The model runs the waves lane by lane in random order and checks
+# that every row the MAC wave reads has been written for every page.
+# ---------------------------------------------------------------------------
+PASS_OFF_BY_ONE = False  # planted mistake: the MAC wave waits for one pass fewer than it needs
+
+
+def small_egress_model(secs, ppw, seed):
+    waves = _const("ztcp_egress.hip", "kSmallWaves") - 1
+    tasks_per_pass = 64 * waves
+    rows = payload_rows(secs)
+    code_rows = [r for r in rows if r[0] == "code"]
+    ncode, nq = len(code_rows), sum(1 for r in rows if r[0] == "scale")
+    ntask = ncode * ppw
+    npass = -(-ntask // tasks_per_pass)
+    written = set()     # (page, payload row) written to the LDS copy
+    passes = [0] * waves
+    done = [0]
+
+    def producer(w):
+        for k in range(npass):
+            lanes = list(range(64))
+            random.Random(seed * 31 + w * 7 + k).shuffle(lanes)
+            for lane in lanes:
+                t = k * tasks_per_pass + w * 64 + lane
+                if t < ntask:
+                    c, i = divmod(t, ppw)
+                    written.add((i, rows.index(code_rows[c])))
+                    yield "step"
+            passes[w] = k + 1
+            yield "step"
+        yield from wait(lambda: min(passes) >= npass)
+        for t in range(w * 64, nq * ppw, tasks_per_pass):
+            for lane_t in range(t, min(t + 64, nq * ppw)):
+                g, i = divmod(lane_t, ppw)
+                written.add((i, rows.index(("scale", g))))
+                yield "step"
+        done[0] += 1
+
+    def mac():
+        ready, scales, c = 0, False, 0
+        for r, row in enumerate(rows):
+            if row[0] == "code":
+                if c >= ready:
+                    need = (c * ppw + ppw - 1) // tasks_per_pass + 1 - (1 if PASS_OFF_BY_ONE else 0)
+                    yield from wait(lambda: min(passes) >= need)
+                    ready = min(ncode, need * tasks_per_pass // ppw)
+                c += 1
+            elif not scales:
+                yield from wait(lambda: done[0] >= waves)
+                scales = True
+            for i in range(ppw):
+                check((i, r) in written, "row read before it was written", r, i, row)
+            yield "step"
+
+    assert Sched(seed).run([mac()] + [producer(w) for w in range(waves)])
+
+
+@pytest.mark.parametrize("cfg", ["k8v4", "int4", "raw_rope", "tiny", "one_unit_sections"])
+@pytest.mark.parametrize("ppw", [1, 2, 3, 4])
+def test_small_egress_passes(cfg, ppw):
+    for seed in range(3):
+        small_egress_model(CONFIGS[cfg], ppw, seed)
+
+
+def test_small_egress_model_catches_a_missing_pass():
+    global PASS_OFF_BY_ONE
+    PASS_OFF_BY_ONE = True
+    try:
+        with pytest.raises(AssertionError, match="before it was written"):
+            for seed in range(20):
+                small_egress_model(CONFIGS["k8v4"], 3, seed)
+    finally:
+        PASS_OFF_BY_ONE = False

@@ -746,6 +746,243 @@ __global__ __launch_bounds__(64 * egress_waves<FAM>()) void egress_fused_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small batches (at most kSmallMaxPpw pages per workgroup, reference kinds).
+// With a few pages per workgroup, lane = page leaves most lanes of the
+// producer waves idle, and each row still costs a whole wave's keystream
+// block: the chain then waits for rows made one page at a time.  Here lane
+// = (code row, page) instead: three producer waves make the code rows of
+// every page 192 at a time (load, quantize, keystream, XOR), write each to
+// the blob and to a copy of the page's whole payload in LDS, and stage its
+// scales; once every code row is made they encrypt the scale rows the same
+// way.  The MAC wave (0, one page per lane) absorbs the payload in order
+// from LDS as the producers' passes complete, two rows of LDS reads ahead,
+// so it never reads global memory and waits only for the first pass.
+// ---------------------------------------------------------------------------
+constexpr int kSmallWaves = 4;        // MAC wave + three producer waves
+constexpr int kSmRowWords = 16;       // one 64-byte payload row of one page
+constexpr int kSmallMaxPpw = 4;       // pages per workgroup up to which the small kernel runs
+constexpr int kSmallTasks = 64 * (kSmallWaves - 1);  // tasks per producer pass
+constexpr int kSmFlagPass = 0;        // [3] passes completed by producer wave 1..3
+constexpr int kSmFlagScales = 3;      // producer waves done with the scale rows
+constexpr int kSmFlagExpired = 4;     // 1: a bounded wait of the workgroup expired
+constexpr int kSmFlags = 16;          // flag words
+constexpr int kSmPay = kSmFlags + kTimerLdsWords;  // the payload copy (64-byte aligned)
+
+// Payload block of the scale row of quantized unit g (staging order).
+__device__ __forceinline__ int32_t scale_block(const Layout& lay, int32_t g) {
+    int32_t blk = 0, q = 0;
+    bool found = false;
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= lay.n_sec || found) continue;
+        if (ZTCP_SEC_FIELD(lay, si, kind) == kSecRaw) continue;
+        const int32_t nu = ZTCP_SEC_FIELD(lay, si, n_units);
+        if (g < q + nu) {
+            blk = (int32_t)(ZTCP_SEC_FIELD(lay, si, s_off) / 64u) + (g - q);
+            found = true;
+        }
+        q += nu;
+    }
+    return blk;
+}
+
+__device__ __forceinline__ void put_row(uint32_t* lds_row, uint8_t* blob_row, const uint32_t (&x)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = make_uint4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+        *reinterpret_cast<uint4*>(lds_row + 4 * q) = v;
+        stg16(blob_row, q, v);
+    }
+}
+
+// Producer wave pw (0..2).  Task t of pass k = 192 k + 64 pw + lane is code
+// row t / ppw of page t % ppw, so a pass holds whole rows of every page.
+template <int DT>
+__device__ void small_produce(const EgressParams& p, int64_t page0, int ppw, int32_t nrow, int32_t nq,
+                              uint32_t* lds, uint64_t t0) {
+    const int pw = (int)(threadIdx.x >> 6) - 1;
+    const int lane = threadIdx.x & 63;
+    uint32_t* flags = lds;
+    uint32_t* pay = lds + kSmPay;
+    uint32_t* stage = pay + (size_t)ppw * nrow * kSmRowWords;
+    const Waiter wt = make_waiter(p.sink, flags + kSmFlagExpired, lds + kSmFlags, t0);
+    const int32_t ntask = total_code_rows(p.lay) * ppw;
+    const int32_t npass = (ntask + kSmallTasks - 1) / kSmallTasks;
+#pragma unroll 1
+    for (int32_t k = 0; k < npass; ++k) {
+        const int32_t t = k * kSmallTasks + pw * 64 + lane;
+        if (t < ntask) {
+            const int32_t i = t % ppw;
+            const Row row = row_info(p.lay, t / ppw);
+            const EgressPage pg = egress_page(p, page0 + i);
+            // both halves' loads first, then the keystream while they are in flight
+            uint32_t w[4][8], w2[4][8], pt[16], sc[4];
+            const bool two = row.s.kind == kSecInt4;
+            load_half(p, pg, row, 0, w);
+            if (two) load_half(p, pg, row, 1, w2);
+            uint32_t ks[16];
+            chacha_block(p.key, 1u + (uint32_t)row.block, (uint32_t)pg.seq, (uint32_t)(pg.seq >> 32), pg.nonce2, ks);
+            quant_first<DT, 0>(row.s.kind, w, pt, sc);
+            uint32_t s2 = 0u, s3 = 0u;
+            if (two) {
+                uint32_t t2[2];
+                quant_half<DT, 4>(w2, pt + 8, t2);
+                s2 = t2[0];
+                s3 = t2[1];
+            }
+#pragma unroll
+            for (int q = 0; q < 16; ++q) ks[q] ^= pt[q];
+            put_row(pay + ((size_t)i * nrow + row.block) * kSmRowWords, pg.blob + kHeader + 64u * (uint32_t)row.block,
+                    ks);
+            // the unit's 16 parameter words: 2 per int8 row, 4 per int4 row
+            uint32_t* st = stage + ((size_t)i * nq + row.g) * kSmRowWords;
+            if (row.s.kind == kSecInt4) {
+                st[4 * row.j + 0] = sc[0];
+                st[4 * row.j + 1] = sc[1];
+                st[4 * row.j + 2] = s2;
+                st[4 * row.j + 3] = s3;
+            } else if (row.s.kind == kSecInt8) {
+                st[2 * row.j + 0] = sc[0];
+                st[2 * row.j + 1] = sc[1];
+            }
+        }
+        publish(&flags[kSmFlagPass + pw], (uint32_t)k + 1u);
+        if constexpr (kPhaseTimers) {
+            if (k == 0) tm_min(wt.tm, kTmProdFirstRow, phase_clock() - t0);
+        }
+    }
+    // scale rows, once every wave has staged all of its scales
+#pragma unroll 1
+    for (int w2 = 0; w2 < kSmallWaves - 1; ++w2) wait_ge<kDiagEgressWait>(&flags[kSmFlagPass + w2], npass, wt);
+    const int32_t nst = nq * ppw;
+#pragma unroll 1
+    for (int32_t t = pw * 64 + lane; t < nst; t += kSmallTasks) {
+        const int32_t i = t % ppw, g = t / ppw;
+        const EgressPage pg = egress_page(p, page0 + i);
+        const int32_t blk = scale_block(p.lay, g);
+        uint32_t ks[16];
+        chacha_block(p.key, 1u + (uint32_t)blk, (uint32_t)pg.seq, (uint32_t)(pg.seq >> 32), pg.nonce2, ks);
+        const uint32_t* st = stage + ((size_t)i * nq + g) * kSmRowWords;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) ks[q] ^= st[q];
+        put_row(pay + ((size_t)i * nrow + blk) * kSmRowWords, pg.blob + kHeader + 64u * (uint32_t)blk, ks);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (lane == 0) __hip_atomic_fetch_add(&flags[kSmFlagScales], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if constexpr (kPhaseTimers) {
+        tm_max(wt.tm, kTmProdLast, phase_clock() - t0);
+        tm_add(wt.tm, kTmProdWaves, 1);
+    }
+}
+
+// The MAC wave: header, then payload rows 0..nrow-1 of page `lane` from LDS.
+// A code row is read once the pass holding its last page's task is complete
+// in all three producer waves, a scale row once every wave has made its
+// scale rows.
+template <int DT>
+__device__ void small_mac(const EgressParams& p, int64_t page0, int ppw, int32_t nrow, uint32_t* lds, uint64_t t0) {
+    const int lane = threadIdx.x & 63;
+    const bool active = lane < ppw;
+    const EgressPage pg = egress_page(p, page0 + (active ? lane : 0));
+    uint32_t* flags = lds;
+    const uint32_t* mine = lds + kSmPay + (size_t)(active ? lane : 0) * nrow * kSmRowWords;
+    if (active) {  // header (cpp:1129-1140)
+        stg16(pg.blob, 0, make_uint4((uint32_t)p.hdr0, (uint32_t)(p.hdr0 >> 32), (uint32_t)pg.hdr1,
+                                     (uint32_t)(pg.hdr1 >> 32)));
+        stg16(pg.blob, 1, make_uint4((uint32_t)pg.token, (uint32_t)(pg.token >> 32), (uint32_t)pg.seq,
+                                     (uint32_t)(pg.seq >> 32)));
+    }
+    Sip s;
+    s.init(p.mk0, p.mk1);
+    const uint64_t hdr[4] = {p.hdr0, pg.hdr1, pg.token, pg.seq};
+    s.absorb_words<4>(hdr);
+    const Waiter wt = make_waiter(p.sink, flags + kSmFlagExpired, lds + kSmFlags, t0);
+    const int32_t ncode = total_code_rows(p.lay);
+    int32_t r = 0;         // payload rows fetched
+    int32_t c = 0;         // code rows absorbed
+    int32_t ready = 0;     // code rows complete for every page
+    bool scales = false;   // scale rows complete
+    auto fetch = [&](uint4 (&x)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[q] = *reinterpret_cast<const uint4*>(mine + r * kSmRowWords + 4 * q);
+        ++r;
+    };
+    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsBegin, phase_clock() - t0);
+    // Sections in payload order, each its code rows then its scale rows; the
+    // code rows in runs that end where the completed passes end, so the
+    // loop itself has no per-row test.
+#pragma unroll 1
+    for (int si = 0; si < 3; ++si) {
+        if (si >= p.lay.n_sec) continue;
+        const int32_t kind = ZTCP_SEC_FIELD(p.lay, si, kind);
+        const int32_t nu = ZTCP_SEC_FIELD(p.lay, si, n_units);
+        int32_t left = nu * code_rows_per_unit(kind);
+#pragma unroll 1
+        while (left > 0) {
+            if (c >= ready) {
+                [[maybe_unused]] const uint64_t t_in = phase_clock();
+                const int32_t need = (c * ppw + ppw - 1) / kSmallTasks + 1;  // passes
+#pragma unroll 1
+                for (int w2 = 0; w2 < kSmallWaves - 1; ++w2)
+                    wait_ge<kDiagEgressWait>(&flags[kSmFlagPass + w2], need, wt);
+                ready = min(ncode, need * kSmallTasks / ppw);
+                if constexpr (kPhaseTimers) {
+                    tm_add(wt.tm, kTmMacWait + min(r >> 6, 7), phase_clock() - t_in);
+                    if (c == 0) tm_add(wt.tm, kTmMacFirstRow, phase_clock() - t0);
+                }
+            }
+            const int32_t n = min(left, ready - c);
+            sip_stream64(s, (uint32_t)n, fetch);
+            c += n;
+            left -= n;
+        }
+        if (kind != kSecRaw) {
+            if (!scales) {
+                [[maybe_unused]] const uint64_t t_in = phase_clock();
+                wait_ge<kDiagEgressWait>(&flags[kSmFlagScales], kSmallWaves - 1, wt);
+                scales = true;
+                if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacWait + min(r >> 6, 7), phase_clock() - t_in);
+            }
+            sip_stream64(s, (uint32_t)nu, fetch);
+        }
+    }
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsEnd, phase_clock() - t0);
+    uint64_t lo, hi;
+    s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
+    if (active)
+        stg16(pg.blob + kHeader + p.payload, 0,
+              make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)));
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacEnd, phase_clock() - t0);
+}
+
+template <int DT>
+__global__ __launch_bounds__(64 * kSmallWaves) void egress_small_kernel(EgressParams p) {
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
+    const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
+    const int32_t nrow = (int32_t)(p.payload / 64u);
+    const int32_t nq = nrow - total_code_rows(p.lay);
+    if (threadIdx.x < kSmFlags) lds[threadIdx.x] = 0u;
+    tm_clear(lds + kSmFlags);
+    __syncthreads();
+    [[maybe_unused]] const uint64_t t0 = phase_clock();
+    [[maybe_unused]] const uint64_t rt0 = kPhaseTimers ? __builtin_amdgcn_s_memrealtime() : 0;
+    if (threadIdx.x < 64) {
+        __builtin_amdgcn_s_setprio(3);
+        small_mac<DT>(p, page0, ppw, nrow, lds, t0);
+    } else {
+        small_produce<DT>(p, page0, ppw, nrow, nq, lds, t0);
+    }
+    // fail closed, as in egress_fused_kernel: the MAC lanes zero the headers
+    __syncthreads();
+    tm_flush(lds + kSmFlags, p.timers, t0, rt0);
+    if (__hip_atomic_load(lds + kSmFlagExpired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u &&
+        (int)threadIdx.x < ppw)
+        stg16(egress_page(p, page0 + threadIdx.x).blob, 0, make_uint4(0u, 0u, 0u, 0u));
+}
+
 }  // namespace
 
 // Zeroes every blob of a call (a synchronous egress whose bounded wait
@@ -765,6 +1002,15 @@ hipError_t launch_egress_zero_blobs(const EgressParams& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// LDS of egress_small_kernel: flags, the payload of every page and the
+// staged parameters of every quantized unit.
+static size_t egress_small_lds_bytes(const EgressParams& p) {
+    int64_t nq = 0;
+    for (int si = 0; si < p.lay.n_sec; ++si)
+        if (p.lay.sec[si].kind != kSecRaw) nq += p.lay.sec[si].n_units;
+    return sizeof(uint32_t) * ((size_t)kSmPay + (size_t)p.ppw * (p.payload / 64u + (size_t)nq) * kSmRowWords);
+}
+
 hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) {
     const int64_t grid = (p.batch + p.ppw - 1) / p.ppw;
     const size_t lds = egress_fused_lds_bytes();  // above 64 KiB: gfx950 has 160 KiB per CU
@@ -773,6 +1019,13 @@ hipError_t launch_egress_fused(const EgressParams& p, int dtype, hipStream_t s) 
         const int32_t kind = p.lay.sec[si].kind;
         if (kind == kSecAsym8 || kind == kSecInt4G32) fam = 2;
         else if (is_extension_kind(kind) && fam < 1) fam = 1;
+    }
+    const size_t small_lds = egress_small_lds_bytes(p);
+    if (fam == 0 && p.ppw <= kSmallMaxPpw && small_lds <= 160u * 1024u) {
+        const dim3 g((uint32_t)grid), b(64 * kSmallWaves);
+        if (dtype == kHotBf16) hipLaunchKernelGGL(egress_small_kernel<kHotBf16>, g, b, small_lds, s, p);
+        else hipLaunchKernelGGL(egress_small_kernel<kHotFp16>, g, b, small_lds, s, p);
+        return hipGetLastError();
     }
     const dim3 g((uint32_t)grid),
         b((uint32_t)(64 * (fam == 0 ? egress_waves<0>() : (fam == 1 ? egress_waves<1>() : egress_waves<2>()))));

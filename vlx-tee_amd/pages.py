@@ -23,19 +23,24 @@ def build_descriptors(k_pages: torch.Tensor, v_pages: torch.Tensor | None, blobs
                       token_hashes: np.ndarray, sequence_nonces: np.ndarray,
                       layer_ids: np.ndarray, head_group_ids: np.ndarray | None = None) -> torch.Tensor:
     """Descriptors for page i = (k_pages[i], v_pages[i], blobs[i], metadata[i]), on the
-    pages' device.  k/v/blobs are contiguous [n, ...] tensors."""
+    pages' device.  Each page of k/v/blobs is contiguous; consecutive pages
+    are k_pages.stride(0) (...) elements apart, so a pool of padded slots
+    (e.g. blob slots rounded up to 128 bytes: ``buf[:, :blob_bytes]``) works."""
     n = k_pages.size(0)
+    for name, t in (("k_pages", k_pages), ("v_pages", v_pages), ("blobs", blobs)):
+        if t is not None and not t[0].is_contiguous():
+            raise ValueError(f"build_descriptors: every page of {name} must be contiguous")
     dt = np.dtype([("k", "<u8"), ("v", "<u8"), ("blob", "<u8"), ("token_hash", "<i8"),
                    ("sequence_nonce", "<u8"), ("layer_id", "<u2"), ("head_group_id", "<u2"),
                    ("reserved", "<u4")])
     assert dt.itemsize == DESC_BYTES
     d = np.zeros(n, dtype=dt)
     idx = np.arange(n, dtype=np.uint64)
-    page_bytes = k_pages[0].numel() * k_pages.element_size()
-    d["k"] = np.uint64(k_pages.data_ptr()) + idx * np.uint64(page_bytes)
+    step = lambda t: np.uint64(t.stride(0) * t.element_size())  # noqa: E731
+    d["k"] = np.uint64(k_pages.data_ptr()) + idx * step(k_pages)
     if v_pages is not None:
-        d["v"] = np.uint64(v_pages.data_ptr()) + idx * np.uint64(page_bytes)
-    d["blob"] = np.uint64(blobs.data_ptr()) + idx * np.uint64(blobs.size(1))
+        d["v"] = np.uint64(v_pages.data_ptr()) + idx * step(v_pages)
+    d["blob"] = np.uint64(blobs.data_ptr()) + idx * step(blobs)
     d["token_hash"] = np.asarray(token_hashes, dtype=np.int64)
     d["sequence_nonce"] = np.asarray(sequence_nonces, dtype=np.uint64)
     d["layer_id"] = np.asarray(layer_ids, dtype=np.uint16)
