@@ -21,7 +21,7 @@ the model follows the constants the kernels are built with.
     wave absorbs rows in payload order; a slot is rewritten only once both
     the MAC wave and the storer have passed it.
   ingress (vlx-tee_amd/csrc/ztcp_ingress.hip): decoders take tasks in order
-    (a unit's scale row two units ahead of its code rows), write code rows
+    (a unit's scale row kLookahead units ahead of its code rows), write code rows
     into the ring, stage decrypted scales; a feeder copies every other
     payload row (scales, padding) into the ring; the verify wave absorbs
     rows in payload order.

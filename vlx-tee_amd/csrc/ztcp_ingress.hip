@@ -12,7 +12,7 @@
 //     flags are not decoded (they fail with status 1).
 //   * Twelve decoder waves (on SIMDs 1-3) take rows in order from an LDS
 //     counter, each with its ciphertext block loaded one row ahead.  A
-//     unit's scale row is decrypted into an LDS staging slot two units ahead
+//     unit's scale row is decrypted into an LDS staging slot four units ahead
 //     of its code rows.  A code row first puts its ciphertext into a ring of
 //     row slots in LDS, at its place in payload order, then decrypts, takes
 //     its scales from staging and dequantizes two groups at a time into a
@@ -49,7 +49,7 @@ constexpr int kIngressThreads = 64 * kIngressWaves;
 constexpr int kDecoderWaves = 12;  // the waves on SIMDs 1-3
 constexpr int kRing = 18;          // payload rows between their makers and the verify wave
 constexpr int kStage = 8;          // units whose decrypted scales are staged at once
-constexpr int kLookahead = 2;      // a unit's scale row is handed out this many units early
+constexpr int kLookahead = 4;      // a unit's scale row is handed out this many units early
 constexpr int kLdsStage = kRing * kRowWords;
 constexpr int kLdsTile = kLdsStage + kStage * kRowWords;       // per decoder wave: 2 groups per page
 constexpr int kLdsFlags = kLdsTile + kDecoderWaves * kRowWords;
