@@ -219,16 +219,20 @@ def test_expired_wait_fails_ingress_closed(env, hip):
     assert torch.equal(ko, e["ref_k"]) and torch.equal(vo, e["ref_v"])
 
 
-def test_expired_wait_fails_egress_closed(env, hip):
+@pytest.mark.parametrize("n", [N_PAGES, 256], ids=["row-pipeline", "small-batch"])
+def test_expired_wait_fails_egress_closed(env, hip, n):
     """Egress whose waits give up fails closed.  Synchronous (the reference's
     form): the call raises KV_INTEGRITY_ERROR with every blob zeroed, before
     any caller could commit the batch (nfc:597-600 zeroes out_blobs on any
     failure).  Asynchronous: the call returns once enqueued, and the blobs of
     the affected workgroups carry a zero header magic, which every ingress
-    rejects with status 1 (cpp:2313-2316)."""
-    e = env
+    rejects with status 1 (cpp:2313-2316).  2,048 pages run the row-pipeline
+    kernel, 256 pages (one per workgroup) the small-batch kernel."""
+    e = dict(env)
+    for key in ("k", "v", "th", "blobs"):
+        e[key] = env[key][:n]
     N, W, keys, w = e["N"], e["W"], e["keys"], e["w"]
-    print("case expired egress wait, synchronous", flush=True)
+    print(f"case expired egress wait, {n} pages, synchronous", flush=True)
     blobs = torch.full_like(e["blobs"], 0xA5)
     prev = hip.debug_spin_limit(0)
     try:
@@ -243,7 +247,7 @@ def test_expired_wait_fails_egress_closed(env, hip):
         g = N.geometry(w.num_tokens, w.num_heads, w.head_dim, w.rope_dim, N.HOT_BF16, False)
         aad = N.Aad(W.TENANT_HASH, W.MODEL_HASH, 0, 0)
         rc = N.lib().ztcp_egress_peak_into_ext(
-            e["k"].data_ptr(), e["v"].data_ptr(), e["th"].data_ptr(), blobs.data_ptr(), N_PAGES, C.byref(g),
+            e["k"].data_ptr(), e["v"].data_ptr(), e["th"].data_ptr(), blobs.data_ptr(), n, C.byref(g),
             w.preset, w.rope_mode, w.payload_bytes, C.byref(aad), 0, C.byref(N.keys(**keys)), N.ASYNC,
             C.c_void_p(torch.cuda.current_stream().cuda_stream))
         assert rc == N.OK
@@ -253,7 +257,7 @@ def test_expired_wait_fails_egress_closed(env, hip):
     assert hip.device_diag() & 1
     assert not blobs[:, :16].any()
     ko, vo = torch.empty_like(e["k"]), torch.empty_like(e["v"])
-    st = torch.full((N_PAGES,), -1, dtype=torch.int32, device="cuda")
+    st = torch.full((n,), -1, dtype=torch.int32, device="cuda")
     with pytest.raises(RuntimeError, match="^KV_INTEGRITY_ERROR: Invalid cold-page header"):
         hip.fused_decode_cold_pages_peak_into(blobs, e["th"], ko, vo, w.rope_dim, False, W.TENANT_HASH,
                                               W.MODEL_HASH, 0, keys["k0"], keys["k1"], keys["mk0"], keys["mk1"],
