@@ -691,6 +691,20 @@ __device__ void ingress_feed(const IngressParams& p, uint32_t* lds, const Layout
     }
 }
 
+// The checks of one page in the reference's order (cpp:2313-2355), given
+// its header words and the xor of the stored and computed tags.
+__device__ __forceinline__ int32_t page_verdict(const IngressParams& p, int64_t page, const uint4 h0, const uint4 h1,
+                                                uint32_t tag_diff) {
+    const uint64_t tok = ingress_token(p, page);
+    const uint32_t layer = ingress_layer(p, page);
+    const uint32_t magic = h0.x & 0xFFFFu, version = (h0.x >> 16) & 0xFFu;
+    if (magic != kMagic || version != kVersion) return 1;
+    if (h0.y != p.exp_tenant || h0.z != p.exp_model || (h0.w & 0xFFFFu) != layer || lo64(h1) != tok) return 2;
+    if (tag_diff != 0u) return 3;
+    if (layout_index(p, h0.x) < 0) return 1;
+    return 0;
+}
+
 // Verdict of one page (cpp:2313-2355).  The payload's full 64-byte rows
 // come from the ring; its last (payload % 64) bytes and the tag are loaded
 // with the header.
@@ -705,8 +719,6 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
 #pragma unroll
     for (int i = 0; i < 3; ++i) tl[i] = ldg16(pay + min(tail0 + 16u * (uint32_t)i, p.payload), 0);
     const uint4 tag = ldg16(pay + p.payload, 0);
-    const uint64_t tok = ingress_token(p, page);
-    const uint32_t layer = ingress_layer(p, page);
     Sip s;
     s.init(p.mk0, p.mk1);
     const uint64_t hdr[4] = {lo64(h0), hi64(h0), lo64(h1), hi64(h1)};
@@ -728,12 +740,92 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     const uint32_t diff = (tag.x ^ (uint32_t)lo) | (tag.y ^ (uint32_t)(lo >> 32)) |
                           (tag.z ^ (uint32_t)hi) | (tag.w ^ (uint32_t)(hi >> 32));
     if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacEnd, phase_clock() - t0);
-    const uint32_t magic = h0.x & 0xFFFFu, version = (h0.x >> 16) & 0xFFu;
-    if (magic != kMagic || version != kVersion) return 1;
-    if (h0.y != p.exp_tenant || h0.z != p.exp_model || (h0.w & 0xFFFFu) != layer || lo64(h1) != tok) return 2;
-    if (diff != 0u) return 3;
-    if (layout_index(p, h0.x) < 0) return 1;
-    return 0;
+    return page_verdict(p, page, h0, h1, diff);
+}
+
+// Pages of a workgroup whose valid layout is not the workgroup's: unit by
+// unit, one page per wave (after the barrier that ends the row pipeline).
+template <int DT, int FAM, int NWAVES>
+__device__ __forceinline__ void decode_other_layouts(const IngressParams& p, int64_t page0, bool active, int li,
+                                                     int li_wg, const uint4 h0, const uint4 h1,
+                                                     const Layout* layouts, uint32_t* nan) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint64_t other = __ballot(active && li >= 0 && li != li_wg);
+    if (other) {
+        int n = 0;
+#pragma unroll 1
+        for (uint64_t m = other; m; m &= m - 1, ++n) {
+            if (n % NWAVES != wave) continue;
+            const int pl = (int)__builtin_ctzll(m);
+            const int lp = __builtin_amdgcn_readlane(li, pl);
+            const Layout& L2 = layouts[lp];
+            const uint32_t a0 = __builtin_amdgcn_readlane(h1.z, pl), a1 = __builtin_amdgcn_readlane(h1.w, pl);
+            const uint32_t a2 = __builtin_amdgcn_readlane(h0.w, pl);
+            const uint32_t m2 = ((a2 & 0xFFFFu) << 16) | (a2 >> 16);
+#pragma unroll 1
+            for (int u = lane; u < L2.n_units; u += 64)
+                decode_unit<DT, FAM>(p, L2, page0 + pl, u, a0, a1, m2, &nan[pl]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // every decode store has completed before the zeroing
+    }
+    __syncthreads();
+}
+
+// The end of an ingress workgroup (every thread): NaN rewrite of verified
+// pages, fail closed after an expired wait, verdicts out, and the per-page
+// policy's zeroing.  status / nan: one word per page of the workgroup (LDS).
+template <int DT>
+__device__ __forceinline__ void ingress_epilogue(const IngressParams& p, int64_t page0, int ppw, uint32_t* status,
+                                                 const uint32_t* nan, const uint32_t* expired_word, uint32_t* tm,
+                                                 uint64_t t0, uint64_t rt0) {
+    // Verified pages with an inf / NaN scale (only possible when |values| pass
+    // 65504 times the code range, so with BF16 data): their NaN outputs are
+    // rewritten as the reference's conversions write them.  Every store to
+    // them has completed (the barriers that end the decode and the other
+    // layouts' decode, before this call).
+#pragma unroll 1
+    for (int pl = 0; pl < ppw; ++pl) {
+        if (nan[pl] == 0u || status[pl] != 0u) continue;
+        const int64_t n16 = p.page_bytes / 16;
+        uint8_t* k = ingress_k(p, page0 + pl);
+        uint8_t* v = ingress_v(p, page0 + pl);
+        for (int64_t i = threadIdx.x; i < 2 * n16; i += blockDim.x) {
+            uint8_t* b = i < n16 ? k : v;
+            if (!b) continue;
+            const uint4 x = ldg16(b, i % n16);
+            uint32_t w[8] = {x.x, x.y, x.z, x.w, 0u, 0u, 0u, 0u};
+            canonical_nans<DT>(w);
+            stg16(b, i % n16, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+    // Fail closed: after an expired bounded wait, a page's verdict and its
+    // decoded bytes may come from rows handed over out of turn, so every page
+    // of the workgroup fails with ZTCP_ERR_DEVICE and its outputs are zeroed
+    // like any failing page's.
+    const bool expired = *expired_word != 0u;
+    if (expired && (int)threadIdx.x < ppw) status[threadIdx.x] = (uint32_t)ZTCP_ERR_DEVICE;
+    __syncthreads();
+    tm_flush(tm, p.timers, t0, rt0);
+    if ((int)threadIdx.x < ppw) {
+        const int32_t st = (int32_t)status[threadIdx.x];
+        const int64_t pg = page0 + threadIdx.x;
+        if (p.page_status) p.page_status[pg] = st;
+        if (st != 0) atomicMin(&p.call->fail, ((unsigned long long)pg << 8) | (unsigned long long)st);
+    }
+    if (p.per_page) {  // extension: zero only the failing pages
+        const int64_t n16 = p.page_bytes / 16;
+#pragma unroll 1
+        for (int pl = 0; pl < ppw; ++pl) {
+            if (status[pl] == 0u) continue;
+            uint8_t* k = ingress_k(p, page0 + pl);
+            for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) stg16(k, i, make_uint4(0, 0, 0, 0));
+            uint8_t* v = ingress_v(p, page0 + pl);
+            if (v)
+                for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) stg16(v, i, make_uint4(0, 0, 0, 0));
+        }
+    }
 }
 
 template <int DT, int FAM>
@@ -803,73 +895,191 @@ __global__ __launch_bounds__(kIngressThreads) void ingress_fused_kernel(IngressP
     }
     __builtin_amdgcn_s_waitcnt(0);  // every row store has completed
     __syncthreads();
-    // pages with another valid layout: unit by unit, one page per wave
-    const uint64_t other = __ballot(active && li >= 0 && li != li_wg);
-    if (other) {
-        int n = 0;
+    decode_other_layouts<DT, FAM, kIngressWaves>(p, page0, active, li, li_wg, h0, h1, layouts, flags + kFlagNaN);
+    ingress_epilogue<DT>(p, page0, ppw, flags + kFlagStatus, flags + kFlagNaN, flags + kFlagExpired,
+                         lds + kLdsTimers, t0, rt0);
+}
+
+// ---------------------------------------------------------------------------
+// Small batches (at most kSiMaxPpw pages per workgroup, the reference's
+// kinds).  As in egress_small_kernel: with lane = page most lanes of the row
+// pipeline idle and the verify wave's chain waits for rows decoded one page
+// at a time.  Here three loader waves copy every payload row of every page
+// into LDS, lane = (row, page), 192 rows per pass, publishing their passes;
+// the verify wave (one page per lane) absorbs the rows from LDS as the passes
+// complete, so its chain runs at the lone rate.  After their load passes the
+// same waves decode the pages with the workgroup's layout, lane = (unit,
+// page), with the unit decoder the row-pipeline kernel uses for pages of
+// another layout (scale row first, then the unit's code rows, from the
+// blobs, which the loads have just brought into L2).  Pages of another valid
+// layout are decoded unit by unit afterwards, and the epilogue is the
+// row-pipeline kernel's.
+// ---------------------------------------------------------------------------
+constexpr int kSiWaves = 4;
+constexpr int kSiMaxPpw = 4;
+constexpr int kSiTasks = 64 * (kSiWaves - 1);  // tasks per pass
+constexpr int kSiRowWords = 16;                // one 64-byte payload row of one page
+constexpr int kSiFlagPass = 0;                 // [3] load passes completed by loader wave 1..3
+constexpr int kSiFlagExpired = 4;              // 1: a bounded wait of the workgroup expired
+constexpr int kSiFlagStatus = 8;               // [4] verdicts
+constexpr int kSiFlagNaN = 12;                 // [4] 1: the page has an inf / NaN scale
+constexpr int kSiFlags = 16;
+constexpr int kSiTimers = kSiFlags;                                     // phase timers (timer builds)
+constexpr int kSiHeaders = kSiTimers + kTimerLdsWords;                  // [4] 32-byte headers
+constexpr int kSiLayouts = kSiHeaders + kSiMaxPpw * 8;                  // [kNumLayouts] Layout
+constexpr int kSiPay = (kSiLayouts + kNumLayouts * kLayoutWords + 15) & ~15;  // payload copies, 64-byte aligned
+static_assert(kSiHeaders % 4 == 0, "header table must be 16-byte aligned");
+
+// Verdict of page `lane` (< ppw) from its payload copy in LDS.
+__device__ __forceinline__ int32_t small_verify(const IngressParams& p, int64_t page0, int ppw, int32_t nrow,
+                                                uint32_t* lds, const uint4 h0, const uint4 h1, uint64_t t0) {
+    const int lane = threadIdx.x & 63;
+    const bool active = lane < ppw;
+    const int64_t page = page0 + (active ? lane : 0);
+    const uint8_t* pay = ingress_blob(p, page) + kHeader;
+    const uint32_t tail0 = (uint32_t)nrow * 64u;
+    const int ntail = (int)((p.payload - tail0) / 16u);  // 0..3 chunks of 16 bytes
+    uint4 tl[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) tl[i] = ldg16(pay + min(tail0 + 16u * (uint32_t)i, p.payload), 0);
+    const uint4 tag = ldg16(pay + p.payload, 0);
+    Sip s;
+    s.init(p.mk0, p.mk1);
+    const uint64_t hdr[4] = {lo64(h0), hi64(h0), lo64(h1), hi64(h1)};
+    s.absorb_words<4>(hdr);
+    uint32_t* flags = lds;
+    const uint32_t* mine = lds + kSiPay + (size_t)(active ? lane : 0) * nrow * kSiRowWords;
+    const Waiter wt = make_waiter(p.sink, flags + kSiFlagExpired, lds + kSiTimers, t0);
+    int32_t r = 0;  // rows fetched
+    auto fetch = [&](uint4 (&x)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[q] = *reinterpret_cast<const uint4*>(mine + r * kSiRowWords + 4 * q);
+        ++r;
+    };
+    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsBegin, phase_clock() - t0);
+    int32_t done = 0, ready = 0;
 #pragma unroll 1
-        for (uint64_t m = other; m; m &= m - 1, ++n) {
-            if (n % kIngressWaves != wave) continue;
-            const int pl = (int)__builtin_ctzll(m);
-            const int lp = __builtin_amdgcn_readlane(li, pl);
-            const Layout& L2 = layouts[lp];
-            const uint32_t a0 = __builtin_amdgcn_readlane(h1.z, pl), a1 = __builtin_amdgcn_readlane(h1.w, pl);
-            const uint32_t a2 = __builtin_amdgcn_readlane(h0.w, pl);
-            const uint32_t m2 = ((a2 & 0xFFFFu) << 16) | (a2 >> 16);
+    while (done < nrow) {
+        if (done >= ready) {  // the pass that loads row `done` of the last page
+            [[maybe_unused]] const uint64_t t_in = phase_clock();
+            const int32_t need = (done * ppw + ppw - 1) / kSiTasks + 1;
 #pragma unroll 1
-            for (int u = lane; u < L2.n_units; u += 64)
-                decode_unit<DT, FAM>(p, L2, page0 + pl, u, a0, a1, m2, &flags[kFlagNaN + pl]);
+            for (int w2 = 0; w2 < kSiWaves - 1; ++w2) wait_ge<kDiagIngressWait>(&flags[kSiFlagPass + w2], need, wt);
+            ready = min(nrow, need * kSiTasks / ppw);
+            if constexpr (kPhaseTimers) {
+                tm_add(wt.tm, kTmMacWait + min(done >> 6, 7), phase_clock() - t_in);
+                if (done == 0) tm_add(wt.tm, kTmMacFirstRow, phase_clock() - t0);
+            }
         }
-        __builtin_amdgcn_s_waitcnt(0);  // every decode store has completed before the zeroing
+        const int32_t n = ready - done;
+        sip_stream64(s, (uint32_t)n, fetch);
+        done += n;
     }
-    __syncthreads();
-    // Verified pages with an inf / NaN scale (only possible when |values| pass
-    // 65504 times the code range, so with BF16 data): their NaN outputs are
-    // rewritten as the reference's conversions write them.  Every store to
-    // them has completed (the two barriers above).
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsEnd, phase_clock() - t0);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (i < ntail) s.absorb(tl[i]);
+    uint64_t lo, hi;
+    s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);
+    const uint32_t diff = (tag.x ^ (uint32_t)lo) | (tag.y ^ (uint32_t)(lo >> 32)) |
+                          (tag.z ^ (uint32_t)hi) | (tag.w ^ (uint32_t)(hi >> 32));
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacEnd, phase_clock() - t0);
+    return page_verdict(p, page, h0, h1, diff);
+}
+
+template <int DT>
+__device__ void small_load_decode(const IngressParams& p, int64_t page0, int ppw, int32_t nrow, uint32_t* lds,
+                                  int li_wg, uint64_t t0) {
+    const int lw = (int)(threadIdx.x >> 6) - 1;
+    const int lane = threadIdx.x & 63;
+    uint32_t* flags = lds;
+    uint32_t* pay = lds + kSiPay;
+    const uint4* hdrs = reinterpret_cast<const uint4*>(lds + kSiHeaders);
+    const Waiter wt = make_waiter(p.sink, flags + kSiFlagExpired, lds + kSiTimers, t0);
+    const int32_t ntask = nrow * ppw;
+    const int32_t npass = (ntask + kSiTasks - 1) / kSiTasks;
 #pragma unroll 1
-    for (int pl = 0; pl < ppw; ++pl) {
-        if (flags[kFlagNaN + pl] == 0u || flags[kFlagStatus + pl] != 0u) continue;
-        const int64_t n16 = p.page_bytes / 16;
-        uint8_t* k = ingress_k(p, page0 + pl);
-        uint8_t* v = ingress_v(p, page0 + pl);
-        for (int64_t i = threadIdx.x; i < 2 * n16; i += blockDim.x) {
-            uint8_t* b = i < n16 ? k : v;
-            if (!b) continue;
-            const uint4 x = ldg16(b, i % n16);
-            uint32_t w[8] = {x.x, x.y, x.z, x.w, 0u, 0u, 0u, 0u};
-            canonical_nans<DT>(w);
-            stg16(b, i % n16, make_uint4(w[0], w[1], w[2], w[3]));
+    for (int32_t k = 0; k < npass; ++k) {
+        const int32_t t = k * kSiTasks + lw * 64 + lane;
+        if (t < ntask) {
+            const int32_t r = t / ppw, i = t - r * ppw;
+            const uint8_t* src = ingress_blob(p, page0 + i) + kHeader + 64u * (uint32_t)r;
+            uint32_t* dst = pay + ((size_t)i * nrow + r) * kSiRowWords;
+            uint4 x[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[q] = ldg16(src, q);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(dst + 4 * q) = x[q];
         }
-        __builtin_amdgcn_s_waitcnt(0);
+        publish(&flags[kSiFlagPass + lw], (uint32_t)k + 1u);
+        if constexpr (kPhaseTimers) {
+            if (k == 0) tm_min(wt.tm, kTmProdFirstRow, phase_clock() - t0);
+        }
     }
-    __syncthreads();
-    // Fail closed: after an expired bounded wait, a page's verdict and its
-    // decoded bytes may come from rows handed over out of turn, so every page
-    // of the workgroup fails with ZTCP_ERR_DEVICE and its outputs are zeroed
-    // like any failing page's.
-    const bool expired = flags[kFlagExpired] != 0u;
-    if (expired && (int)threadIdx.x < ppw) flags[kFlagStatus + threadIdx.x] = (uint32_t)ZTCP_ERR_DEVICE;
-    __syncthreads();
-    tm_flush(lds + kLdsTimers, p.timers, t0, rt0);
+    if (li_wg >= 0) {
+        // the units of the pages with the workgroup's layout, lane = (unit,
+        // page), from the blobs (in L2 since the loads above)
+        const Layout& lay = reinterpret_cast<const Layout*>(lds + kSiLayouts)[li_wg];
+        const int32_t ntask2 = lay.n_units * ppw;
+#pragma unroll 1
+        for (int32_t t = lw * 64 + lane; t < ntask2; t += kSiTasks) {
+            const int32_t u = t / ppw, i = t - u * ppw;
+            const uint4 h0 = hdrs[2 * i], h1 = hdrs[2 * i + 1];
+            if (layout_index(p, h0.x) != li_wg) continue;
+            const uint32_t n2 = ((h0.w & 0xFFFFu) << 16) | (h0.w >> 16);  // nonce (cpp:2357-2365)
+            decode_unit<DT, 0>(p, lay, page0 + i, u, h1.z, h1.w, n2, &flags[kSiFlagNaN + i]);
+        }
+    }
+    if constexpr (kPhaseTimers) {
+        tm_max(wt.tm, kTmProdLast, phase_clock() - t0);
+        tm_add(wt.tm, kTmProdWaves, 1);
+    }
+}
+
+// One workgroup per CU at most (grid = batch / pages per workgroup <= CU
+// count), one wave per SIMD: registers need not be shared.
+template <int DT>
+__global__ __launch_bounds__(64 * kSiWaves) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void ingress_small_kernel(IngressParams p) {
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int64_t page0 = (int64_t)blockIdx.x * p.ppw;
+    const int ppw = (int)min((int64_t)p.ppw, p.batch - page0);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool active = lane < ppw;
+    const int32_t nrow = (int32_t)(p.payload / 64u);
+    uint32_t* flags = lds;
+    uint4* hdrs = reinterpret_cast<uint4*>(lds + kSiHeaders);
     if ((int)threadIdx.x < ppw) {
-        const int32_t st = (int32_t)flags[kFlagStatus + threadIdx.x];
-        const int64_t pg = page0 + threadIdx.x;
-        if (p.page_status) p.page_status[pg] = st;
-        if (st != 0) atomicMin(&p.call->fail, ((unsigned long long)pg << 8) | (unsigned long long)st);
+        const uint8_t* b = ingress_blob(p, page0 + threadIdx.x);
+        hdrs[2 * threadIdx.x] = ldg16(b, 0);
+        hdrs[2 * threadIdx.x + 1] = ldg16(b, 1);
     }
-    if (p.per_page) {  // extension: zero only the failing pages
-        const int64_t n16 = p.page_bytes / 16;
-#pragma unroll 1
-        for (int pl = 0; pl < ppw; ++pl) {
-            if (flags[kFlagStatus + pl] == 0u) continue;
-            uint8_t* k = ingress_k(p, page0 + pl);
-            for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) stg16(k, i, make_uint4(0, 0, 0, 0));
-            uint8_t* v = ingress_v(p, page0 + pl);
-            if (v)
-                for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) stg16(v, i, make_uint4(0, 0, 0, 0));
-        }
+    Layout* layouts = reinterpret_cast<Layout*>(lds + kSiLayouts);
+    if (threadIdx.x < kNumLayouts) layouts[threadIdx.x] = ingress_layout(p, (int)threadIdx.x);
+    if (threadIdx.x < kSiFlags) flags[threadIdx.x] = 0u;
+    tm_clear(lds + kSiTimers);
+    __syncthreads();
+    [[maybe_unused]] const uint64_t t0 = phase_clock();
+    [[maybe_unused]] const uint64_t rt0 = kPhaseTimers ? __builtin_amdgcn_s_memrealtime() : 0;
+    // every wave derives the workgroup layout from the headers itself
+    const int lp = active ? lane : 0;
+    const uint4 h0 = hdrs[2 * lp], h1 = hdrs[2 * lp + 1];
+    const int li = layout_index(p, h0.x);
+    const uint64_t any_valid = __ballot(active && li >= 0);
+    const int li_wg = any_valid ? __builtin_amdgcn_readlane(li, (int)__builtin_ctzll(any_valid)) : -1;
+    if (wave == 0) {
+        __builtin_amdgcn_s_setprio(3);
+        const int32_t v = small_verify(p, page0, ppw, nrow, lds, h0, h1, t0);
+        if (active) flags[kSiFlagStatus + lane] = (uint32_t)v;
+    } else {
+        small_load_decode<DT>(p, page0, ppw, nrow, lds, li_wg, t0);
     }
+    __builtin_amdgcn_s_waitcnt(0);  // every decode store has completed
+    __syncthreads();
+    decode_other_layouts<DT, 0, kSiWaves>(p, page0, active, li, li_wg, h0, h1, layouts, flags + kSiFlagNaN);
+    ingress_epilogue<DT>(p, page0, ppw, flags + kSiFlagStatus, flags + kSiFlagNaN, flags + kSiFlagExpired,
+                         lds + kSiTimers, t0, rt0);
 }
 
 }  // namespace
@@ -900,6 +1110,14 @@ hipError_t launch_ingress_fused(const IngressParams& p, int dtype, hipStream_t s
     // family 1 (the extension kinds) only when the call enables the extension layouts
     const bool ext = (p.lay_ok >> 12) != 0u;  // bits of presets 4..6 (index (preset - 1) * 4 + rope_mode)
     const bool ext_rope = (p.lay_ok & 0x888u) != 0u;  // RoPE mode 3 of presets 1..3
+    // small batches of the reference's kinds: every page's payload in LDS
+    const size_t small_lds = sizeof(uint32_t) * ((size_t)kSiPay + (size_t)p.ppw * (p.payload / 64u) * kSiRowWords);
+    if (!ext && !ext_rope && p.ppw <= kSiMaxPpw && small_lds <= 160u * 1024u) {
+        const dim3 g((uint32_t)grid), b(64 * kSiWaves);
+        if (dtype == kHotBf16) hipLaunchKernelGGL(ingress_small_kernel<kHotBf16>, g, b, small_lds, s, p);
+        else hipLaunchKernelGGL(ingress_small_kernel<kHotFp16>, g, b, small_lds, s, p);
+        return hipGetLastError();
+    }
     if (dtype == kHotBf16) {
         if (ext || ext_rope)
             hipLaunchKernelGGL((ingress_fused_kernel<kHotBf16, 1>), dim3((uint32_t)grid), dim3(kIngressThreads), lds, s, p);

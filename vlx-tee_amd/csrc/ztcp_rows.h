@@ -216,7 +216,9 @@ __device__ __forceinline__ void wait_ge(const uint32_t* flag, int32_t want, cons
             if ((threadIdx.x & 63) == 0) {
                 atomicOr(w.dev_diag, DIAG);
                 if (w.call_diag) {
-                    if (w.call_tag) atomicMax(w.call_diag, w.call_tag);
+                    // egress calls carry a tag (the host reads the slot back
+                    // by tag); ingress calls or in their kernel's bit
+                    if constexpr (DIAG == kDiagEgressWait) atomicMax(w.call_diag, w.call_tag);
                     else atomicOr(w.call_diag, DIAG);
                 }
             }
@@ -478,6 +480,44 @@ __device__ __forceinline__ int32_t total_code_rows(const Layout& lay) {
         t += ZTCP_SEC_FIELD(lay, si, n_units) * code_rows_per_unit(kind);
     }
     return t;
+}
+
+// One code row of a layout, by its index among the page's code rows.
+struct Row {
+    int32_t valid;
+    int32_t u, j;     // unit in section, code block in unit
+    int32_t g;        // unit index among the page's quantized units (staging slot order)
+    int32_t cidx;     // code row index = production order
+    int32_t mrow;     // row index in the MAC wave's order (code rows and scale rows)
+    int32_t block;    // payload block index (keystream counter - 1)
+    SecRows s;
+};
+
+// Code row t: the payload's code blocks in order (egress: also the order of
+// production).
+__device__ __forceinline__ Row row_info(const Layout& lay, int32_t t) {
+    Row row{};
+    int32_t cb = 0, qb = 0;
+#pragma unroll
+    for (int si = 0; si < 3; ++si) {
+        if (si >= lay.n_sec || row.valid) continue;
+        const SecRows s = sec_rows(lay, si, cb, qb);
+        const int32_t n = s.n_units * s.nblk;
+        if (t >= cb && t < cb + n) {
+            const int32_t local = t - cb;
+            row.valid = 1;
+            row.u = local / s.nblk;  // nblk is 8, 4 or 16
+            row.j = local - row.u * s.nblk;
+            row.g = s.qunit_begin + row.u;
+            row.cidx = t;
+            row.mrow = t + qb;  // the scale rows of earlier sections come first
+            row.block = (int32_t)(s.q_off / 64u) + local;
+            row.s = s;
+        }
+        cb += n;
+        if (s.kind != kSecRaw) qb += s.n_units;
+    }
+    return row;
 }
 
 }  // namespace ztcp
