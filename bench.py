@@ -241,13 +241,13 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float, timers: bool =
     return res
 
 
-def run_small_egress(wname: str, steps: int) -> dict:
-    """Egress only of a small batch (the reference's peak-256 case,
-    research/benchmarks/bench_cold_page_pipeline.py:924-930): pages in HBM,
-    blobs into a preallocated buffer.  Timed twice: back to back, with the
-    8 MiB of hot pages resident in the caches ("warm"), and with the caches
-    flushed before every launch by writing a 1 GiB buffer ("flushed"); HIP
-    events bracket the egress launch alone."""
+def run_small(wname: str, steps: int) -> dict:
+    """Egress and ingress of a small batch (the reference's peak-256 case,
+    research/benchmarks/bench_cold_page_pipeline.py:924-930), each launch
+    timed alone: pages in HBM, blobs and outputs preallocated.  Timed twice:
+    back to back, with the 8 MiB of hot pages resident in the caches
+    ("warm"), and with the caches flushed before every launch by writing a
+    1 GiB buffer ("flushed"); HIP events bracket the launch alone."""
     import torch
 
     _package().load_native()
@@ -260,7 +260,10 @@ def run_small_egress(wname: str, steps: int) -> dict:
     k, v = generate(w, dev, torch.bfloat16)
     th, seq, layers = page_metadata(w)
     blobs = torch.empty((w.n_pages, w.blob_bytes), dtype=torch.uint8, device=dev)
+    ko, vo = torch.empty_like(k), torch.empty_like(v)
+    status = torch.full((w.n_pages,), -1, dtype=torch.int32, device=dev)
     d = P.build_descriptors(k, v, blobs, th, seq, layers)
+    d_in = P.build_descriptors(ko, vo, blobs, th, seq, layers)
     geo = dict(num_tokens=w.num_tokens, num_heads=w.num_heads, head_dim=w.head_dim,
                rope_dim=w.rope_dim, dtype=torch.bfloat16, is_mla_single_buffer=w.mla)
 
@@ -269,38 +272,46 @@ def run_small_egress(wname: str, steps: int) -> dict:
                  expected_payload_bytes=w.payload_bytes, tenant_id_hash=TENANT_HASH,
                  model_id_hash=MODEL_HASH, ext_layouts=w.extension, asynchronous=True, **geo, **keys)
 
+    def ingress():
+        P.ingress(d_in, w.n_pages, w.blob_bytes, expected_tenant_hash=TENANT_HASH,
+                  expected_model_hash=MODEL_HASH, page_status=status, asynchronous=True,
+                  ext_layouts=w.extension, **geo, **keys)
+
     egress()
     torch.cuda.synchronize()
     ref = blobs.clone()
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
-    warm, cold = [], []
+    times = {(f, c): [] for f in ("egress", "ingress") for c in ("warm", "flushed")}
     for i in range(3 + steps):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        egress()
-        b.record(stream)
-        flush.fill_(i & 0xFF)
-        c, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        c.record(stream)
-        egress()
-        e.record(stream)
-        torch.cuda.synchronize()
-        if i >= 3:
-            warm.append(a.elapsed_time(b))
-            cold.append(c.elapsed_time(e))
+        for name, fn in (("egress", egress), ("ingress", ingress)):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            flush.fill_(i & 0xFF)
+            c, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            c.record(stream)
+            fn()
+            e.record(stream)
+            torch.cuda.synchronize()
+            if i >= 3:
+                times[(name, "warm")].append(a.elapsed_time(b))
+                times[(name, "flushed")].append(c.elapsed_time(e))
     if not torch.equal(ref, blobs):
         raise SystemExit(f"bench: {wname} egress is not deterministic")
+    if not bool((status == 0).all()):
+        raise SystemExit(f"bench: {wname} pages failed verification")
     hot = w.n_pages * w.hot_bytes_per_page
     wire = w.n_pages * w.blob_bytes
-    mw, mc = statistics.mean(warm), statistics.mean(cold)
-    res = dict(workload=wname, pages=w.n_pages, hot_bytes=hot, wire_bytes=wire, direction="egress only",
-               egress_ms_warm=mw, egress_ms_flushed=mc,
-               egress_hot_gbps_warm=hot / mw / 1e6, egress_wire_gbps_warm=wire / mw / 1e6,
-               egress_hot_gbps_flushed=hot / mc / 1e6, egress_wire_gbps_flushed=wire / mc / 1e6,
-               note=("one page per workgroup (256 of the 256 CUs): the launch lasts one page's "
-                     "SipHash chain, 1541 words in sequence"))
-    del k, v, blobs, flush, ref
+    res = dict(workload=wname, pages=w.n_pages, hot_bytes=hot, wire_bytes=wire, direction="egress and ingress")
+    for (name, cache), t in times.items():
+        m = statistics.mean(t)
+        res[f"{name}_ms_{cache}"] = m
+        res[f"{name}_hot_gbps_{cache}"] = hot / m / 1e6
+    res["note"] = ("one page per workgroup (256 workgroups on 256 CUs), small-batch kernels: each launch lasts "
+                   "about one page's SipHash chain, 1541 words in sequence")
+    del k, v, blobs, flush, ref, ko, vo
     torch.cuda.empty_cache()
     return res
 
@@ -528,7 +539,7 @@ def main() -> None:
                                        "c3_e4m3_tamper,c4_mla_int4g32"),
                     help="comma list of extra workloads")
     ap.add_argument("--small", default="c1_int4_gqa256",
-                    help="comma list of small egress-only workloads (warm and cache-flushed)")
+                    help="comma list of small workloads, egress and ingress timed apart (warm and cache-flushed)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--settle-seconds", type=float, default=0.3,
                     help="untimed egress + ingress pairs before the warmup steps (clock leaves idle)")
@@ -565,7 +576,7 @@ def main() -> None:
     for wn in [x for x in a.also.split(",") if x and x != a.workload]:
         extras[wn] = run_gpu(wn, max(3, a.steps // 2), 2, a.settle_seconds / 2)
     for wn in [x for x in a.small.split(",") if x]:
-        extras[wn] = run_small_egress(wn, max(5, a.steps))
+        extras[wn] = run_small(wn, max(5, a.steps))
     wire_ring = None if a.no_wire else run_wire_ring(a.workload)
     cpu = None if a.no_cpu else cpu_baseline(a.workload, a.cpu_seconds)
 
