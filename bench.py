@@ -243,11 +243,12 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float, timers: bool =
 
 def run_small(wname: str, steps: int) -> dict:
     """Egress and ingress of a small batch (the reference's peak-256 case,
-    research/benchmarks/bench_cold_page_pipeline.py:924-930), each launch
-    timed alone: pages in HBM, blobs and outputs preallocated.  Timed twice:
-    back to back, with the 8 MiB of hot pages resident in the caches
-    ("warm"), and with the caches flushed before every launch by writing a
-    1 GiB buffer ("flushed"); HIP events bracket the launch alone."""
+    research/benchmarks/bench_cold_page_pipeline.py:924-930), each direction
+    timed apart: pages in HBM, blobs and outputs preallocated.  Timed twice:
+    launches back to back, with the 8 MiB of hot pages resident in the
+    caches ("warm", the mean per launch), and each launch after the caches
+    were flushed by writing a 1 GiB buffer ("flushed", HIP events around the
+    launch alone)."""
     import torch
 
     _package().load_native()
@@ -282,13 +283,22 @@ def run_small(wname: str, steps: int) -> dict:
     ref = blobs.clone()
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
+    # warm: `steps` launches back to back between one pair of events (the
+    # launches are queued while the GPU works, so no host gap is timed);
+    # flushed: each launch queued behind a 1 GiB fill, between its own events
     times = {(f, c): [] for f in ("egress", "ingress") for c in ("warm", "flushed")}
-    for i in range(3 + steps):
-        for name, fn in (("egress", egress), ("ingress", ingress)):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
+    for name, fn in (("egress", egress), ("ingress", ingress)):
+        for _ in range(3):
             fn()
-            b.record(stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        flush.fill_(0)  # keeps the GPU busy while the launches below are queued
+        a.record(stream)
+        for _ in range(steps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        times[(name, "warm")].append(a.elapsed_time(b) / steps)
+        for i in range(3 + steps):
             flush.fill_(i & 0xFF)
             c, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             c.record(stream)
@@ -296,7 +306,6 @@ def run_small(wname: str, steps: int) -> dict:
             e.record(stream)
             torch.cuda.synchronize()
             if i >= 3:
-                times[(name, "warm")].append(a.elapsed_time(b))
                 times[(name, "flushed")].append(c.elapsed_time(e))
     if not torch.equal(ref, blobs):
         raise SystemExit(f"bench: {wname} egress is not deterministic")
