@@ -156,6 +156,26 @@ def check(cond, *msg):
     assert cond, msg
 
 
+MAC_GROUP_OFF = False  # planted mistake: the MAC wave tests only the first row of each group
+
+
+def mac_groups(prow, ring, ring_flag, st, KRING):
+    """The MAC / verify wave (mac_rows, vlx-tee_amd/csrc/ztcp_rows.h): rows
+    in groups of kMacGroup; a group is read once every row of it is in the
+    ring, and `used` is published once per group."""
+    G = _const("ztcp_rows.h", "kMacGroup")
+    assert KRING % G == 0, "ring lengths are multiples of the MAC group"
+    for g0 in range(0, len(prow), G):
+        rows = range(g0, min(g0 + G, len(prow)))
+        for m in (rows[:1] if MAC_GROUP_OFF else rows):
+            yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
+        for m in rows:
+            check(ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m]))
+            yield "ok"
+        st["used"] = rows[-1] + 1
+        yield "ok"
+
+
 def egress_model(secs, n_prod, seed):
     KRING, KSTAGE = _const("ztcp_egress.hip", "kRing"), _const("ztcp_egress.hip", "kStage")
     prow = payload_rows(secs)
@@ -253,11 +273,7 @@ def egress_model(secs, n_prod, seed):
             yield "ok"
 
     def mac():
-        for m in range(len(prow)):
-            yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
-            check(ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m]))
-            st["used"] = m + 1
-            yield "ok"
+        yield from mac_groups(prow, ring, ring_flag, st, KRING)
 
     return Sched(seed).run([producer() for _ in range(n_prod)] + [feeder(), mac(), storer()])
 
@@ -403,11 +419,7 @@ def ingress_model(secs, n_dec, seed, padding=0):
             yield "ok"
 
     def verify():
-        for m in range(len(prow)):
-            yield from wait(lambda: ring_flag[m % KRING] >= m + 1)
-            check(ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m]))
-            st["used"] = m + 1
-            yield "ok"
+        yield from mac_groups(prow, ring, ring_flag, st, KRING)
 
     return Sched(seed).run([decoder() for _ in range(n_dec)] + [feeder(), verify()])
 
@@ -635,3 +647,14 @@ def test_small_egress_model_catches_a_missing_pass():
                 small_egress_model(CONFIGS["k8v4"], 3, seed)
     finally:
         PASS_OFF_BY_ONE = False
+
+
+def test_model_catches_a_group_read_on_its_first_flag_only():
+    global MAC_GROUP_OFF
+    MAC_GROUP_OFF = True
+    try:
+        with pytest.raises(AssertionError):
+            for seed in range(20):
+                egress_model(CONFIGS["k8v4"], 11, seed)
+    finally:
+        MAC_GROUP_OFF = False

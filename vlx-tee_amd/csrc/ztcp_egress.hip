@@ -61,7 +61,7 @@ namespace {
 // memory.
 template <int FAM>
 constexpr int egress_waves() { return FAM <= 1 ? 16 : 12; }  // family 2's quantizers need 168 VGPRs
-constexpr int kRing = 30;             // payload rows between their makers and the MAC wave
+constexpr int kRing = 28;             // payload rows between their makers and the MAC wave
 constexpr int kStage = 8;             // units whose scales are staged at once
 constexpr int kLdsStage = kRing * kRowWords;
 constexpr int kScaleSlots = 64;       // scale rows the feeder wave may still be waiting for
@@ -512,7 +512,7 @@ __device__ void egress_mac(const EgressParams& p, int64_t page0, int ppw, uint32
     __builtin_amdgcn_s_waitcnt(0);
     if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsBegin, phase_clock() - t0);
     mac_rows<kRing, kDiagEgressWait>(wt, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
-                                     m.total, [](int32_t, int, const uint4&) {});
+                                     m.total);
     if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacRowsEnd, phase_clock() - t0);
     uint64_t lo, hi;
     s.finish((uint64_t)((kHeader + p.payload) & 0xFFu) << 56, lo, hi);

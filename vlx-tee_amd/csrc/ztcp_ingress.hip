@@ -47,7 +47,7 @@ namespace {
 constexpr int kIngressWaves = 16;
 constexpr int kIngressThreads = 64 * kIngressWaves;
 constexpr int kDecoderWaves = 12;  // the waves on SIMDs 1-3
-constexpr int kRing = 18;          // payload rows between their makers and the verify wave
+constexpr int kRing = 16;          // payload rows between their makers and the verify wave
 constexpr int kStage = 8;          // units whose decrypted scales are staged at once
 constexpr int kLookahead = 4;      // a unit's scale row is handed out this many units early
 constexpr int kLdsStage = kRing * kRowWords;
@@ -730,7 +730,7 @@ __device__ __forceinline__ int32_t verify_page(const IngressParams& p, int64_t p
     __builtin_amdgcn_s_waitcnt(0);
     if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacRowsBegin, phase_clock() - t0);
     mac_rows<kRing, kDiagIngressWait>(st, lds, lds + kLdsFlags + kFlagRing, lds + kLdsFlags + kFlagMacUsed, pq, s,
-                                      total, [](int32_t, int, const uint4&) {});
+                                      total);
     if constexpr (kPhaseTimers) tm_add(st.tm, kTmMacRowsEnd, phase_clock() - t0);
 #pragma unroll
     for (int i = 0; i < 3; ++i)

@@ -275,117 +275,108 @@ __device__ __forceinline__ void set_row_priority(int32_t lead) {
 // wave publishes `used` = rows absorbed, which frees their slots.
 // ---------------------------------------------------------------------------
 
-// One fetched row: its 64 bytes for this lane's page and the value of the
-// row's ready flag, read just before the data.  LDS operations of a wave are
-// performed in order, and a row's maker writes it before it releases the
-// row's flag; so when the flag read shows the row, the data read after it
-// holds the row.  Otherwise the row is read again once the flag is set.
-struct MacRow {
-    uint4 x[4];
-    uint32_t f;
-    int32_t slot;  // ring slot (wave-uniform)
-};
+// Rows per readiness test and per release of the MAC / verify wave.  Ring
+// lengths are multiples of it, so a group's four flags are one aligned
+// 16-byte LDS read.  Against a test and a release per row this takes about
+// 70 clocks per row off the chain (a probe of the MAC wave alone in the
+// kernel: 1,836 clocks per row with per-row flags and releases, 1,790
+// without the flag reads, 1,808 without the releases).
+constexpr int kMacGroup = 4;
 
-__device__ __forceinline__ void mac_fetch(const uint32_t* ring, const uint32_t* ring_flags, const PageQuads& pq,
-                                          int32_t slot, MacRow& r) {
-    r.slot = slot;
-    r.f = __hip_atomic_load(ring_flags + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+// The four ready flags of the group at `slot`, read before any of the
+// group's data (LDS operations of a wave are performed in order, and a row's
+// maker writes the row before it releases its flag: a flag read that shows
+// the row guarantees that a later data read holds it).
+__device__ __forceinline__ uint4 mac_flags4(const uint32_t* ring_flags, int32_t slot) {
+    const u32x4 v = *reinterpret_cast<const volatile u32x4*>(ring_flags + slot);
     asm volatile("" ::: "memory");  // the data reads stay after the flag read
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + slot * kRowWords, pq.off[q]);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Absorbs payload row `want - 1` and releases its slot.  `ready` says
-// whether the row's flag read already showed the row; otherwise the row is
-// read again once the flag is set.  The previous row's quads (in `prev`, when
-// has_prev) go to on_quad(row, q, quad) one at a time after words 0, 2, 4, 6
-// of this row: memory instructions spread over the chain cost it nothing,
-// while four in a row stall the wave on the address unit.
-template <uint32_t DIAG, class OnQuad>
-__device__ __forceinline__ void mac_absorb(const Waiter& wt, const uint32_t* ring, const uint32_t* ring_flags,
-                                           uint32_t* used, const PageQuads& pq, Sip& s, MacRow& r, int32_t want,
-                                           bool ready, OnQuad& on_quad, const MacRow& prev, bool has_prev) {
-    if (__builtin_expect(!ready, 0)) {
-        [[maybe_unused]] const uint64_t t_in = phase_clock();
-        wait_ge<DIAG>(ring_flags + r.slot, want, wt);
-        [[maybe_unused]] const uint64_t t_flag = phase_clock();
+// Whether rows row0 .. row0 + 3 (those below total) are all in the ring.
+// Every lane read the same words: a vector compare and a ballot cost the
+// chain nothing measurable, where v_readfirstlane of a flag cost it about
+// 66 clocks.
+__device__ __forceinline__ bool mac_ready4(const uint4 f, int32_t row0, int32_t total) {
+    const bool ok = ((int32_t)f.x > row0 || row0 >= total) && ((int32_t)f.y > row0 + 1 || row0 + 1 >= total) &&
+                    ((int32_t)f.z > row0 + 2 || row0 + 2 >= total) && ((int32_t)f.w > row0 + 3 || row0 + 3 >= total);
+    return __builtin_amdgcn_ballot_w64(!ok) == 0ull;
+}
+
+__device__ __forceinline__ void mac_row_data(const uint32_t* ring, const PageQuads& pq, int32_t slot, uint4 (&x)[4]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) r.x[q] = lds_quad_at(ring + r.slot * kRowWords, pq.off[q]);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
+    for (int q = 0; q < 4; ++q) x[q] = lds_quad_at(ring + slot * kRowWords, pq.off[q]);
+}
+
+// Absorbs payload rows [0, total) from a ring of RING slots, four rows per
+// group.  The group's flags are read, then the data of its first two rows,
+// while the previous group's last two rows are absorbed; at the group's
+// start one ballot tests all four flags (if any row is missing the wave
+// waits for each and reads the first two rows again); the data of its third
+// and fourth rows are read while its first two are absorbed.  Every read
+// thus has two rows' absorption to complete before it is used, and the
+// wave publishes `used` once per group.  Reads past the last row fetch
+// slots that are never absorbed.  The caller completes every load it has
+// issued before the call: a load still counted as in flight where the loop
+// begins would turn the loop's LDS waits into full waits.
+template <int RING, uint32_t DIAG>
+__device__ __forceinline__ void mac_rows(const Waiter& wt, const uint32_t* ring, const uint32_t* ring_flags,
+                                         uint32_t* used, const PageQuads& pq, Sip& s, int32_t total) {
+    static_assert(RING % kMacGroup == 0 && kMacGroup == 4, "a group's flags are one aligned 16-byte read");
+    uint4 b0[4], b1[4], b2[4], b3[4];
+    int32_t gs = 0;  // ring slot of the group's first row
+    uint4 fl = mac_flags4(ring_flags, 0);
+    mac_row_data(ring, pq, 0, b0);
+    mac_row_data(ring, pq, 1, b1);
+    [[maybe_unused]] auto traced = [&](int32_t row) {
         if constexpr (kPhaseTimers) {
-            const uint64_t t_out = phase_clock();
-            const int b = min((want - 1) >> 6, 7);
-            tm_add(wt.tm, kTmMacWait + b, t_out - t_in);
-            tm_add(wt.tm, kTmMacMiss + b, 1);
-            if (wt.trace && (threadIdx.x & 63) == 0 && want <= kTraceRows) {
-                wt.trace[2 * kTraceRows + want - 1] = (uint32_t)(t_flag - t_in);
-                wt.trace[3 * kTraceRows + want - 1] = (uint32_t)(t_out - t_flag);
+            if (row == 0) tm_add(wt.tm, kTmMacFirstRow, phase_clock() - wt.t0);
+            tm_trace(wt.trace, kTraceRows + row, wt.t0);
+        }
+    };
+#pragma unroll 1
+    for (int32_t r = 0; r < total; r += kMacGroup) {
+        if (__builtin_expect(!mac_ready4(fl, r, total), 0)) {
+            [[maybe_unused]] const uint64_t t_in = phase_clock();
+#pragma unroll
+            for (int i = 0; i < kMacGroup; ++i)
+                if (r + i < total) wait_ge<DIAG>(ring_flags + gs + i, r + i + 1, wt);
+            [[maybe_unused]] const uint64_t t_flag = phase_clock();
+            mac_row_data(ring, pq, gs, b0);
+            mac_row_data(ring, pq, gs + 1, b1);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
+            if constexpr (kPhaseTimers) {
+                const uint64_t t_out = phase_clock();
+                const int b = min(r >> 6, 7);
+                tm_add(wt.tm, kTmMacWait + b, t_out - t_in);
+                tm_add(wt.tm, kTmMacMiss + b, 1);
+                if (wt.trace && (threadIdx.x & 63) == 0 && r < kTraceRows) {
+                    wt.trace[2 * kTraceRows + r] = (uint32_t)(t_flag - t_in);
+                    wt.trace[3 * kTraceRows + r] = (uint32_t)(t_out - t_flag);
+                }
             }
         }
+        const int32_t ns = gs + kMacGroup == RING ? 0 : gs + kMacGroup;
+        mac_row_data(ring, pq, gs + 2, b2);
+        s.absorb64(b0);
+        traced(r);
+        if (r + 1 >= total) break;
+        mac_row_data(ring, pq, gs + 3, b3);
+        s.absorb64(b1);
+        traced(r + 1);
+        if (r + 2 >= total) break;
+        fl = mac_flags4(ring_flags, ns);
+        mac_row_data(ring, pq, ns, b0);
+        s.absorb64(b2);
+        traced(r + 2);
+        if (r + 3 >= total) break;
+        mac_row_data(ring, pq, ns + 1, b1);
+        s.absorb64(b3);
+        traced(r + 3);
+        publish(used, (uint32_t)(r + kMacGroup));
+        gs = ns;
     }
-    s.absorb64_with(r.x, [&](int i) {
-        if ((i & 1) == 0 && has_prev) on_quad(want - 2, i >> 1, prev.x[i >> 1]);
-    });
-    publish(used, (uint32_t)want);
-    if constexpr (kPhaseTimers) {
-        if (want == 1) tm_add(wt.tm, kTmMacFirstRow, phase_clock() - wt.t0);
-        tm_trace(wt.trace, kTraceRows + want - 1, wt.t0);
-    }
-}
-
-// Every lane read the same flag word.  A vector compare and a ballot cost the
-// chain nothing measurable, where a v_readfirstlane of the flag cost it
-// about 66 clocks per row (4 % of the row).
-__device__ __forceinline__ bool mac_ready(const MacRow& r, int32_t want) {
-    return __builtin_amdgcn_ballot_w64((int32_t)r.f < want) == 0ull;
-}
-
-// Absorbs payload rows [0, total) from a ring of RING slots.  Three row
-// buffers rotate: two rows are in flight while one is absorbed, and a buffer
-// is fetched again one absorption after the one that read it, so every read
-// has a whole row's absorption to complete before it is used and no wait
-// lands on a fresh read; a row's quads go to on_quad during the next row's
-// absorption, from the buffer that still holds it.  A row's ready
-// flag is tested right after the previous row's slot is released (a release
-// waits for every LDS operation issued before it, so the flag value is there
-// already), never at the loop head, where the wait would also cover the
-// fetch just issued.  Fetches are unconditional (past the last row they read
-// slots that are never absorbed): a fetch under a branch would leave the
-// buffer in different registers on the two paths, and the copy that joins
-// them would wait for the fresh read.  The caller completes every load it
-// has issued before the call: a load still counted as in flight where the
-// loop begins (a scalar load in particular, as those complete out of order)
-// would turn the loop's LDS waits into full waits.
-template <int RING, uint32_t DIAG, class OnQuad>
-__device__ __forceinline__ void mac_rows(const Waiter& st, const uint32_t* ring, const uint32_t* ring_flags,
-                                         uint32_t* used, const PageQuads& pq, Sip& s, int32_t total,
-                                         OnQuad&& on_quad) {
-    MacRow r0, r1, r2;
-    int32_t slot = 0;
-    auto next_slot = [&]() { const int32_t v = slot; slot = slot == RING - 1 ? 0 : slot + 1; return v; };
-    // the last absorbed row's quads, once no row follows to carry them
-    auto flush = [&](const MacRow& r, int32_t row) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) on_quad(row, q, r.x[q]);
-    };
-    mac_fetch(ring, ring_flags, pq, next_slot(), r0);
-    mac_fetch(ring, ring_flags, pq, next_slot(), r1);
-    bool ok0 = mac_ready(r0, 1);
-#pragma unroll 1
-    for (int32_t c = 0; c < total; c += 3) {
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r0, c + 1, ok0, on_quad, r2, c > 0);
-        const bool ok1 = mac_ready(r1, c + 2);
-        mac_fetch(ring, ring_flags, pq, next_slot(), r2);
-        if (c + 1 >= total) { flush(r0, c); break; }
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r1, c + 2, ok1, on_quad, r0, true);
-        const bool ok2 = mac_ready(r2, c + 3);
-        mac_fetch(ring, ring_flags, pq, next_slot(), r0);
-        if (c + 2 >= total) { flush(r1, c + 1); break; }
-        mac_absorb<DIAG>(st, ring, ring_flags, used, pq, s, r2, c + 3, ok2, on_quad, r1, true);
-        ok0 = mac_ready(r0, c + 4);
-        mac_fetch(ring, ring_flags, pq, next_slot(), r1);
-        if (c + 3 >= total) { flush(r2, c + 2); break; }
-    }
+    publish(used, (uint32_t)total);  // a last partial group
 }
 
 // ---------------------------------------------------------------------------
