@@ -377,6 +377,21 @@ struct DecoderCtx {
     uint32_t tq0;
 
     __device__ __forceinline__ void init_stores() { tq0 = quad_word(lane >> 2, lane & 3) * 4u; }
+
+    // 16 on odd lanes, else 0: the second quad of the 32 bytes that a lane
+    // pair stores.  Bits 4-5 of tq0 are (lane & 3) ^ ((lane >> 3) & 3) and
+    // bit 7 is (lane >> 3) & 1, so bit 4 of tq0 ^ (tq0 >> 3) is lane & 1.
+    // Recomputed at each store by instructions the compiler cannot hoist: a
+    // value held across the task loop is one VGPR more than the BF16 kernel
+    // of the extension kinds has at 16 waves, and the allocator spills it
+    // (a scratch reload, which waits for every load in flight).
+    __device__ __forceinline__ uint32_t odd16() const {
+        uint32_t r;
+        asm volatile("v_lshrrev_b32 %0, 3, %1\n\tv_xor_b32 %0, %0, %1\n\tv_and_b32 %0, 16, %0"
+                     : "=&v"(r)
+                     : "v"(tq0));
+        return r;
+    }
 };
 
 template <int DT, int KIND>
@@ -453,7 +468,7 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
         const uint32_t off_b = cur.off;
         cur.step(k.s.gpv, skip);
         // lanes 4i, 4i + 1 store the first group's two quads, 4i + 2, 4i + 3 the second's
-        const uint32_t off = ((c.lane & 2) ? off_b : off_a) + 16u * (uint32_t)(c.lane & 1);
+        const uint32_t off = ((c.lane & 2) ? off_b : off_a) + c.odd16();
         const uint64_t* ptab = reinterpret_cast<const uint64_t*>(c.lds + kLdsPtrs) + (to_v ? 64 : 0) + (c.lane >> 2);
         uint4 x[4];
         uint8_t* out[4];
@@ -524,7 +539,7 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
         cur.step(k.s.gpv, skip);
         const uint32_t off_b = cur.off;
         cur.step(k.s.gpv, skip);
-        const uint32_t off = ((c.lane & 2) ? off_b : off_a) + 16u * (uint32_t)(c.lane & 1);
+        const uint32_t off = ((c.lane & 2) ? off_b : off_a) + c.odd16();
         const uint64_t* ptab = reinterpret_cast<const uint64_t*>(c.lds + kLdsPtrs) + (to_v ? 64 : 0) + (c.lane >> 2);
         uint4 x[4];
         uint8_t* out[4];
