@@ -215,3 +215,40 @@ def test_ext_special_values(hip, O, dtype):
         err, st, gk, gv, rc, ost, ok, ov = _ingress(hip, O, got, th, (T, Hh, D), R, mla, DT[dtype])
         assert err is None and rc == 0
         assert np.array_equal(gk, ok) and np.array_equal(gv, ov), (preset, rm)
+
+
+def _asym8_tie_groups(fp16: bool):
+    """64-element groups whose codes (and, fp16 only, zero point) fall on
+    exact ties: scale 1/16 (range 255/16), values (2k + 1) / 32."""
+    k = np.arange(62)
+    ties = (2 * k + 1) / 32.0
+    groups = [np.concatenate([[0.0, 255 / 16], ties]), np.concatenate([[0.0, -255 / 16], -ties])]
+    if fp16:
+        groups.append(np.concatenate([[-253 / 32, 257 / 32], ties[:31], -ties[:31]]))
+    return groups
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_ext_asym8_ties(hip, O, dtype):
+    """asym8 groups on exact rounding ties (codes and zero points round to
+    even in the oracle, tests/test_oracle_ext.py): the kernels' codes, blobs
+    and decoded pages equal the oracle's."""
+    T, Hh, D, R, mla, B = 16, 4, 128, 64, False, 8
+    k, v = _pages(29, B, T, Hh, D, R, mla, DT[dtype])
+    groups = _asym8_tie_groups(dtype == "fp16")
+    kf = k.float()
+    i = 0
+    for b in range(B):
+        for t in range(0, T, 3):
+            for h in range(Hh):
+                kf[b, t, h, R:] = torch.from_numpy(groups[i % len(groups)].astype(np.float32))
+                i += 1
+    k = kf.to(DT[dtype])
+    assert torch.equal(k.float()[0, 0, 0, R:], torch.from_numpy(groups[0].astype(np.float32)))
+    th = np.arange(B, dtype=np.int64) + 40
+    for preset, rm in [(4, 3), (4, 1)]:
+        got, want = _egress(hip, O, k, v, th, preset, rm, R)
+        assert np.array_equal(got, want), (preset, rm)
+        err, st, gk, gv, rc, ost, ok, ov = _ingress(hip, O, got, th, (T, Hh, D), R, mla, DT[dtype])
+        assert err is None and rc == 0 and (st == 0).all()
+        assert np.array_equal(gk, ok) and np.array_equal(gv, ov), (preset, rm)

@@ -13,7 +13,8 @@ restate it:
     equal), plus the error bound;
   * asymmetric int8 per 64: invariants a plausible mistake breaks (zero is
     exact, codes span [0, 255] from the group minimum to its maximum, the
-    error bound, the scale by numpy's division and float16 rounding);
+    error bound, the scale by numpy's division and float16 rounding), and
+    exact ties of codes and zero points, which must round to even;
   * page sizing and byte maps: section offsets computed from the format, and
     the decrypted payload compared with group-wise quantization.
 """
@@ -178,6 +179,40 @@ def test_asym8_g64_invariants(dtype):
     assert (outf[zero_in] == 0).all()
     tol = s[:, None] * 0.5 * (1 + 2.0 ** -8) + np.abs(x) * 2.0 ** -7 + s[:, None] * 2.0 ** -10
     assert (np.abs(outf - x) <= tol).all()
+
+
+@pytest.mark.parametrize("dtype", [O.FP16, O.BF16])
+def test_asym8_g64_ties_round_to_even(dtype):
+    """Codes and zero points that fall exactly halfway between two integers
+    round to the even one.  Groups whose range is 255 / 16 get the scale
+    1 / 16 exactly (an fp16 power of two, so v * inv is exact), and values
+    (2k + 1) / 32 then sit on the tie k + 1/2; a half-away-from-zero or
+    truncating rounding fails here, where the invariants above cannot see it."""
+    k = np.arange(128)
+    ties = (2 * k + 1) / 32.0                       # v * 16 = k + 1/2
+    even = np.where(k % 2 == 0, k, k + 1)           # the even neighbour
+    # all-positive group: lo = 0, hi = 255/16, z = 0
+    pos = np.concatenate([[0.0, 255 / 16], ties[:62]])
+    # all-negative values with hi = 0: lo = -255/16, z = 255; -(k + 1/2) -> -even
+    neg = np.concatenate([[0.0, -255 / 16], -ties[:62]])
+    groups = [pos, neg]
+    want_q = [np.concatenate([[0, 255], even[:62]]),
+              np.concatenate([[255, 0], 255 - even[:62]])]
+    want_z = [0, 255]
+    if dtype == O.FP16:
+        # the zero point on a tie: lo = -253/32 (-lo * 16 = 126.5 -> 126),
+        # hi = 257/32 (hi * 16 = 128.5 -> 128, code 254), so the range is
+        # 510/32 = 255/16 again
+        mixed = np.concatenate([[-253 / 32, 257 / 32], ties[:31], -ties[:31]])
+        groups.append(mixed)
+        want_z.append(126)
+        want_q.append(np.concatenate([[0, 254], 126 + even[:31], 126 - even[:31]]))
+    src = np.stack([_hot(np.asarray(g, dtype=np.float32), dtype) for g in groups])
+    assert (_hot_f32(src, dtype) == np.stack(groups).astype(np.float32)).all()  # exactly representable
+    q, prm = O.quant_groups_ext(src, dtype, O.SEC_ASYM8)
+    assert (prm[:, 0] == np.float16(1 / 16).view(np.uint16)).all()
+    np.testing.assert_array_equal(prm[:, 1], want_z)
+    np.testing.assert_array_equal(q.astype(np.int64), np.stack(want_q))
 
 
 # ---- sizing, byte maps and round trips ------------------------------------------
