@@ -327,6 +327,10 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
     ChaChaState st;
     st.start_cached(p.key, c.nc, 1u + (uint32_t)row.block);
     st.double_rounds<4>();
+    // the priority is refreshed after four and after seven double rounds;
+    // pin_words keeps the rounds on their side of each refresh
+    pin_words(st.x);
+    refresh_row_priority(&flags[kFlagMacUsed], row.mrow);
     // the second half's scale words go to variables of their own: stores
     // into sc at other indices than the first half's let the compiler merge
     // the two quantizer calls into one store at a runtime index, which puts
@@ -342,7 +346,10 @@ __device__ __forceinline__ void code_row(const ProducerCtx& c, const Row& row, c
         s2 = quant_half_int4g32<DT>(w, pt + 8);
     }
     if (nxt.valid) load_half_any<FAM>(p, c.pg, nxt, 0, w);
-    st.double_rounds<5>();
+    st.double_rounds<3>();
+    pin_words(st.x);
+    refresh_row_priority(&flags[kFlagMacUsed], row.mrow);
+    st.double_rounds<2>();
     if (kind != kSecRaw) {
         // the unit's staging slot is free once unit g - kStage's scale row is done
         uint32_t* stage = c.lds + kLdsStage + (row.g % kStage) * kRowWords;

@@ -356,6 +356,12 @@ __device__ __forceinline__ int32_t total_tasks(const Layout& lay) {
     return t;
 }
 
+// The payload row that sets a task's urgency: a code task's own row; a
+// scale task is as urgent as the first code row of its unit.
+__device__ __forceinline__ int32_t task_lead_row(const Task& k) {
+    return k.scale ? (int32_t)(k.s.q_off / 64u) + k.u * k.s.nblk : k.mrow;
+}
+
 struct DecoderCtx {
     const IngressParams* p;
     const uint8_t* pay;     // this lane's page payload
@@ -409,6 +415,8 @@ __device__ __forceinline__ void code_task(const DecoderCtx& c, const Task& k, ui
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
     publish(&flags[kFlagRing + k.mrow % kRing], (uint32_t)k.mrow + 1u);
     tm_trace(c.wt.trace, k.mrow, c.wt.t0);
+    // this row is out: the rest of the task runs at the urgency of the next
+    if (nxt.valid) refresh_row_priority(&flags[kFlagMacUsed], task_lead_row(nxt));
     uint32_t pt[16];
     {
         uint32_t ks[16];
@@ -497,6 +505,8 @@ __device__ __forceinline__ void code_task_ext(const DecoderCtx& c, const Task& k
         lds_put_quad_at(slot, c.pq.off[q], make_uint4(ct[4 * q], ct[4 * q + 1], ct[4 * q + 2], ct[4 * q + 3]));
     publish(&flags[kFlagRing + k.mrow % kRing], (uint32_t)k.mrow + 1u);
     tm_trace(c.wt.trace, k.mrow, c.wt.t0);
+    // this row is out: the rest of the task runs at the urgency of the next
+    if (nxt.valid) refresh_row_priority(&flags[kFlagMacUsed], task_lead_row(nxt));
     uint32_t pt[16];
     {
         uint32_t ks[16];
@@ -607,8 +617,7 @@ __device__ __forceinline__ void decode_rows(const DecoderCtx& c, const Layout& l
         if constexpr (kPhaseTimers) {
             if (made++ == 1) tm_min(c.wt.tm, kTmProdFirstRow, phase_clock() - c.wt.t0);
         }
-        // a scale row is as urgent as the first code row of its unit
-        set_row_priority((k.scale ? (int32_t)(k.s.q_off / 64u) + k.u * k.s.nblk : k.mrow) - used);
+        set_row_priority(task_lead_row(k) - used);
         const Task nxt = task_info<FAM>(lay, tn);
         if (k.scale)
             scale_task(c, k, ct, nxt);

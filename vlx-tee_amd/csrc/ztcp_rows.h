@@ -269,6 +269,17 @@ __device__ __forceinline__ void set_row_priority(int32_t lead) {
     else __builtin_amdgcn_s_setprio(0);
 }
 
+// set_row_priority for payload row `row` from the rows absorbed so far.
+// Workers call it again while they make a row: a row taken far ahead of the
+// MAC / verify wave starts at a low priority, and if its wave is the
+// youngest on its SIMD it is starved by the older ones until it is the row
+// that holds up the chain (a group of rows waiting for its last member).
+__device__ __forceinline__ void refresh_row_priority(const uint32_t* used, int32_t row) {
+    set_row_priority(
+        row - (int32_t)__builtin_amdgcn_readfirstlane(
+                  __hip_atomic_load(used, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)));
+}
+
 // ---------------------------------------------------------------------------
 // The MAC wave's side of a ring of row slots holding the payload in order:
 // payload row r sits in slot r % ring_len once flag[slot] = r + 1, and the
