@@ -214,10 +214,9 @@ def run_gpu(wname: str, steps: int, warmup: int, settle_s: float, timers: bool =
         phase = dict(egress=summarize_phase_timers(N.phase_timers(0)),
                      ingress=summarize_phase_timers(N.phase_timers(1)))
         for d, name in ((0, "egress"), (1, "ingress")):
-            arrive, absorb, wait_flag, reread = N.phase_trace(d)
+            arrive, absorb, group_wait, _ = N.phase_trace(d)
             phase[name]["trace_wg0"] = dict(arrive=arrive[:rows].tolist(), absorb=absorb[:rows].tolist(),
-                                            slow_flag_wait=wait_flag[:rows].tolist(),
-                                            slow_reread=reread[:rows].tolist())
+                                            group_wait=group_wait[:rows].tolist())
     hot = w.n_pages * w.hot_bytes_per_page
     wire = w.n_pages * w.blob_bytes
     me, mi = statistics.mean(te), statistics.mean(ti)

@@ -45,12 +45,12 @@ ZTCP_API int64_t ztcp_phase_timers_read(int32_t direction, uint64_t* out, int64_
 /* Workgroup 0's row trace of the same launch: 4 * ZTCP_TRACE_ROWS 32-bit
  * words.  Clocks since its first barrier: out[r] when payload row r reached
  * the ring, out[ZTCP_TRACE_ROWS + r] when the MAC / verify wave absorbed it;
- * for a row whose ready flag that wave found unset when it fetched the row,
- * the clocks it then waited for the flag (out[2 * ZTCP_TRACE_ROWS + r]) and
- * for the re-read of the row's data (out[3 * ZTCP_TRACE_ROWS + r]); rows
- * past the payload, and the last two words of fast-path rows, keep whatever
- * an earlier launch left there.  Returns 4 * ZTCP_TRACE_ROWS, 0 when no fused
- * launch was recorded, or a negative ZTCP_E* code. */
+ * for a group of four rows starting at r whose ready flags that wave found
+ * incomplete, the clocks it then waited for the group's rows
+ * (out[2 * ZTCP_TRACE_ROWS + r], zero for every other row);
+ * out[3 * ZTCP_TRACE_ROWS + r] is zero.  Rows past the payload keep whatever
+ * an earlier launch left in the first two words.  Returns 4 * ZTCP_TRACE_ROWS,
+ * 0 when no fused launch was recorded, or a negative ZTCP_E* code. */
 ZTCP_API int64_t ztcp_phase_trace_read(int32_t direction, uint32_t* out, int64_t max_words);
 
 #ifdef __cplusplus

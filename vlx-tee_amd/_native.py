@@ -205,7 +205,8 @@ def phase_timers(direction: int):
 def phase_trace(direction: int):
     """Workgroup 0's row trace of the last fused launch of `direction`:
     uint32 arrays of TRACE_ROWS (ring arrival clocks, absorption clocks,
-    slow-path flag wait, slow-path re-read)."""
+    at the first row of each group of four that was not ready: the clocks
+    waited for its rows; a fourth array of zeros)."""
     import numpy as np
 
     L = lib()

@@ -130,10 +130,10 @@ __device__ __forceinline__ void tm_clear(uint32_t* tm) {
 }
 // Workgroup 0's row trace (timer builds): 32-bit clocks since the first
 // barrier at which each payload row reached the ring (trace[r]) and at which
-// the MAC / verify wave absorbed it (trace[kTraceRows + r]); for rows whose
-// flag the MAC / verify wave found unset when it fetched them, the clocks it
-// then waited for the flag (trace[2 kTraceRows + r]) and for the data's
-// re-read (trace[3 kTraceRows + r]).
+// the MAC / verify wave absorbed it (trace[kTraceRows + r]); for a group of
+// four rows from r whose flags that wave found incomplete, the clocks it
+// then waited for the group's rows (trace[2 kTraceRows + r]); the words from
+// 3 kTraceRows stay zero.
 __device__ __forceinline__ uint32_t* trace_of(unsigned long long* timers) {
     if constexpr (kPhaseTimers) {
         if (timers && blockIdx.x == 0)
@@ -322,11 +322,11 @@ __device__ __forceinline__ void mac_row_data(const uint32_t* ring, const PageQua
 // Absorbs payload rows [0, total) from a ring of RING slots, four rows per
 // group.  The group's flags are read, then the data of its first two rows,
 // while the previous group's last two rows are absorbed; at the group's
-// start one ballot tests all four flags (if any row is missing the wave
-// waits for each and reads the first two rows again); the data of its third
-// and fourth rows are read while its first two are absorbed.  Every read
-// thus has two rows' absorption to complete before it is used, and the
-// wave publishes `used` once per group.  Reads past the last row fetch
+// start one ballot tests all four flags (if any row is missing, the wave
+// takes that group a row at a time, below); the data of its third and
+// fourth rows are read while its first two are absorbed.  Every read thus
+// has two rows' absorption to complete before it is used, and the wave
+// publishes `used` once per group.  Reads past the last row fetch
 // slots that are never absorbed.  The caller completes every load it has
 // issued before the call: a load still counted as in flight where the loop
 // begins would turn the loop's LDS waits into full waits.
@@ -347,27 +347,39 @@ __device__ __forceinline__ void mac_rows(const Waiter& wt, const uint32_t* ring,
     };
 #pragma unroll 1
     for (int32_t r = 0; r < total; r += kMacGroup) {
-        if (__builtin_expect(!mac_ready4(fl, r, total), 0)) {
-            [[maybe_unused]] const uint64_t t_in = phase_clock();
-#pragma unroll
-            for (int i = 0; i < kMacGroup; ++i)
-                if (r + i < total) wait_ge<DIAG>(ring_flags + gs + i, r + i + 1, wt);
-            [[maybe_unused]] const uint64_t t_flag = phase_clock();
-            mac_row_data(ring, pq, gs, b0);
-            mac_row_data(ring, pq, gs + 1, b1);
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the re-read is complete on both paths
-            if constexpr (kPhaseTimers) {
-                const uint64_t t_out = phase_clock();
-                const int b = min(r >> 6, 7);
-                tm_add(wt.tm, kTmMacWait + b, t_out - t_in);
-                tm_add(wt.tm, kTmMacMiss + b, 1);
-                if (wt.trace && (threadIdx.x & 63) == 0 && r < kTraceRows) {
-                    wt.trace[2 * kTraceRows + r] = (uint32_t)(t_flag - t_in);
-                    wt.trace[3 * kTraceRows + r] = (uint32_t)(t_out - t_flag);
-                }
-            }
-        }
         const int32_t ns = gs + kMacGroup == RING ? 0 : gs + kMacGroup;
+        if (__builtin_expect(!mac_ready4(fl, r, total), 0)) {
+            // A row of the group is missing (most often its last, held by a
+            // worker that fell behind): take the group a row at a time, each
+            // as soon as it is in the ring, and release each slot at once,
+            // so that the rows already there are absorbed while the wave
+            // waits for the missing one.
+            [[maybe_unused]] uint64_t waited = 0;
+#pragma unroll 1
+            for (int i = 0; i < kMacGroup; ++i) {
+                if (r + i >= total) break;
+                [[maybe_unused]] const uint64_t t_in = phase_clock();
+                wait_ge<DIAG>(ring_flags + gs + i, r + i + 1, wt);
+                if constexpr (kPhaseTimers) waited += phase_clock() - t_in;
+                mac_row_data(ring, pq, gs + i, b2);
+                s.absorb64(b2);
+                traced(r + i);
+                publish(used, (uint32_t)(r + i + 1));
+            }
+            if constexpr (kPhaseTimers) {
+                const int b = min(r >> 6, 7);
+                tm_add(wt.tm, kTmMacWait + b, waited);
+                tm_add(wt.tm, kTmMacMiss + b, 1);
+                if (wt.trace && (threadIdx.x & 63) == 0 && r < kTraceRows)
+                    wt.trace[2 * kTraceRows + r] = (uint32_t)waited;
+            }
+            if (r + kMacGroup >= total) break;
+            fl = mac_flags4(ring_flags, ns);
+            mac_row_data(ring, pq, ns, b0);
+            mac_row_data(ring, pq, ns + 1, b1);
+            gs = ns;
+            continue;
+        }
         mac_row_data(ring, pq, gs + 2, b2);
         s.absorb64(b0);
         traced(r);
