@@ -176,13 +176,15 @@ __device__ __forceinline__ uint64_t add_u64(uint64_t a, uint64_t b) {
     return r;
 }
 // rotl(a, 32) + b, with the rotation done by reading a's halves exchanged.
+// The carry goes through VCC in one asm block: with the carry in an SGPR
+// pair the compiler put a wait state (s_nop) between the two halves, a few
+// hundred per workgroup's chain.
 __device__ __forceinline__ uint64_t add_rot32_u64(uint64_t a, uint64_t b) {
     uint32_t lo, hi;
-    uint64_t c, c2;
-    asm("v_add_co_u32 %0, %1, %2, %3" : "=v"(lo), "=s"(c) : "v"((uint32_t)(a >> 32)), "v"((uint32_t)b));
-    asm("v_addc_co_u32 %0, %1, %2, %3, %4"
-        : "=v"(hi), "=s"(c2)
-        : "v"((uint32_t)a), "v"((uint32_t)(b >> 32)), "s"(c));
+    asm("v_add_co_u32_e32 %0, vcc, %2, %3\n\tv_addc_co_u32_e32 %1, vcc, %4, %5, vcc"
+        : "=&v"(lo), "=v"(hi)
+        : "v"((uint32_t)(a >> 32)), "v"((uint32_t)b), "v"((uint32_t)a), "v"((uint32_t)(b >> 32))
+        : "vcc");
     return ((uint64_t)hi << 32) | lo;
 }
 __device__ __forceinline__ uint64_t rot32_u64(uint64_t a) { return (a << 32) | (a >> 32); }
