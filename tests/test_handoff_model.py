@@ -164,13 +164,14 @@ def mac_groups(prow, ring, ring_flag, st, KRING):
     in groups of kMacGroup.  One test of the group's flags: a group whose rows
     are all in the ring is read at once and `used` is published once for it;
     otherwise the group is taken a row at a time, each row once its flag is
-    set, and `used` is published after each."""
+    set, and `used` is published after each.  The last total % kMacGroup
+    rows are always taken a row at a time."""
     G = _const("ztcp_rows.h", "kMacGroup")
     assert KRING % G == 0, "ring lengths are multiples of the MAC group"
     for g0 in range(0, len(prow), G):
         rows = range(g0, min(g0 + G, len(prow)))
         tested = rows[:1] if MAC_GROUP_OFF else rows
-        if all(ring_flag[m % KRING] >= m + 1 for m in tested):
+        if len(rows) == G and all(ring_flag[m % KRING] >= m + 1 for m in tested):
             for m in rows:
                 check(ring[m % KRING] == prow[m], (m, ring[m % KRING], prow[m]))
                 yield "ok"

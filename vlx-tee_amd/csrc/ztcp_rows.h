@@ -345,61 +345,75 @@ __device__ __forceinline__ void mac_rows(const Waiter& wt, const uint32_t* ring,
             tm_trace(wt.trace, kTraceRows + row, wt.t0);
         }
     };
+    // A row taken alone: waited for, read, absorbed and released at once.
+    auto one_row = [&](int32_t row, int32_t slot, uint64_t& waited) {
+        [[maybe_unused]] const uint64_t t_in = phase_clock();
+        wait_ge<DIAG>(ring_flags + slot, row + 1, wt);
+        if constexpr (kPhaseTimers) waited += phase_clock() - t_in;
+        mac_row_data(ring, pq, slot, b2);
+        s.absorb64(b2);
+        traced(row);
+        publish(used, (uint32_t)(row + 1));
+    };
+    // Whole groups.  The inner loop takes ready groups and has one exit, to
+    // the code for a group with a row missing, which rejoins it with the
+    // next group's flags and first two rows in fl, b0 and b1, as the inner
+    // loop leaves them.  (A loop with its exits between the rows of a group
+    // had the compiler copy the chain's state and the prefetched rows to
+    // other registers and back on every iteration.)
+    const int32_t full = total & ~(kMacGroup - 1);
+    int32_t r = 0;
 #pragma unroll 1
-    for (int32_t r = 0; r < total; r += kMacGroup) {
-        const int32_t ns = gs + kMacGroup == RING ? 0 : gs + kMacGroup;
-        if (__builtin_expect(!mac_ready4(fl, r, total), 0)) {
-            // A row of the group is missing (most often its last, held by a
-            // worker that fell behind): take the group a row at a time, each
-            // as soon as it is in the ring, and release each slot at once,
-            // so that the rows already there are absorbed while the wave
-            // waits for the missing one.
-            [[maybe_unused]] uint64_t waited = 0;
+    while (r < full) {
 #pragma unroll 1
-            for (int i = 0; i < kMacGroup; ++i) {
-                if (r + i >= total) break;
-                [[maybe_unused]] const uint64_t t_in = phase_clock();
-                wait_ge<DIAG>(ring_flags + gs + i, r + i + 1, wt);
-                if constexpr (kPhaseTimers) waited += phase_clock() - t_in;
-                mac_row_data(ring, pq, gs + i, b2);
-                s.absorb64(b2);
-                traced(r + i);
-                publish(used, (uint32_t)(r + i + 1));
-            }
-            if constexpr (kPhaseTimers) {
-                const int b = min(r >> 6, 7);
-                tm_add(wt.tm, kTmMacWait + b, waited);
-                tm_add(wt.tm, kTmMacMiss + b, 1);
-                if (wt.trace && (threadIdx.x & 63) == 0 && r < kTraceRows)
-                    wt.trace[2 * kTraceRows + r] = (uint32_t)waited;
-            }
-            if (r + kMacGroup >= total) break;
+        for (; r < full; r += kMacGroup) {
+            if (__builtin_expect(!mac_ready4(fl, r, total), 0)) break;
+            const int32_t ns = gs + kMacGroup == RING ? 0 : gs + kMacGroup;
+            mac_row_data(ring, pq, gs + 2, b2);
+            s.absorb64(b0);
+            traced(r);
+            mac_row_data(ring, pq, gs + 3, b3);
+            s.absorb64(b1);
+            traced(r + 1);
             fl = mac_flags4(ring_flags, ns);
             mac_row_data(ring, pq, ns, b0);
+            s.absorb64(b2);
+            traced(r + 2);
             mac_row_data(ring, pq, ns + 1, b1);
+            s.absorb64(b3);
+            traced(r + 3);
+            publish(used, (uint32_t)(r + kMacGroup));
             gs = ns;
-            continue;
         }
-        mac_row_data(ring, pq, gs + 2, b2);
-        s.absorb64(b0);
-        traced(r);
-        if (r + 1 >= total) break;
-        mac_row_data(ring, pq, gs + 3, b3);
-        s.absorb64(b1);
-        traced(r + 1);
-        if (r + 2 >= total) break;
+        if (r >= full) break;
+        // A row of the group is missing (most often its last, held by a
+        // worker that fell behind): take the group a row at a time, each as
+        // soon as it is in the ring, and release each slot at once, so that
+        // the rows already there are absorbed while the wave waits for the
+        // missing one.
+        const int32_t ns = gs + kMacGroup == RING ? 0 : gs + kMacGroup;
+        [[maybe_unused]] uint64_t waited = 0;
+#pragma unroll 1
+        for (int i = 0; i < kMacGroup; ++i) one_row(r + i, gs + i, waited);
+        if constexpr (kPhaseTimers) {
+            const int b = min(r >> 6, 7);
+            tm_add(wt.tm, kTmMacWait + b, waited);
+            tm_add(wt.tm, kTmMacMiss + b, 1);
+            if (wt.trace && (threadIdx.x & 63) == 0 && r < kTraceRows)
+                wt.trace[2 * kTraceRows + r] = (uint32_t)waited;
+        }
         fl = mac_flags4(ring_flags, ns);
         mac_row_data(ring, pq, ns, b0);
-        s.absorb64(b2);
-        traced(r + 2);
-        if (r + 3 >= total) break;
         mac_row_data(ring, pq, ns + 1, b1);
-        s.absorb64(b3);
-        traced(r + 3);
-        publish(used, (uint32_t)(r + kMacGroup));
         gs = ns;
+        r += kMacGroup;
     }
-    publish(used, (uint32_t)total);  // a last partial group
+    // the last total % 4 rows, one at a time
+    [[maybe_unused]] uint64_t waited = 0;
+#pragma unroll 1
+    for (int32_t i = 0; r < total; ++r, ++i) one_row(r, gs + i, waited);
+    if constexpr (kPhaseTimers) tm_add(wt.tm, kTmMacWait + min(full >> 6, 7), waited);
+    publish(used, (uint32_t)total);
 }
 
 // ---------------------------------------------------------------------------
