@@ -81,6 +81,9 @@ def summarize_phase_timers(rec) -> dict:
         start_spread_us=round(float((col("real_start").max() - col("real_start").min()) / 100), 2),
         launch_span_us=round(float((col("real_end").max() - col("real_start").min()) / 100), 2),
         wg_clocks=m(col("wg_end")), wg_clocks_max=round(float(col("wg_end").max()), 1),
+        # workgroup 0 also writes the row trace, which slows it down
+        wg_clocks_max_untraced=round(float(col("wg_end")[1:].max()), 1) if r.shape[0] > 1 else None,
+        wg_clocks_p90=round(float(np.percentile(col("wg_end"), 90)), 1),
         mac=dict(rows_begin=m(col("mac_rows_begin")), first_row=m(col("mac_first_row")),
                  rows_end=m(col("mac_rows_end")), end=m(col("mac_end")),
                  wait_total=m(sum(col("mac_wait", i) for i in range(8))),
