@@ -324,3 +324,27 @@ def test_kat_hooks_on_gpu(hip, O):
 def test_fast_quantizer_arithmetic_selftest(hip):
     """Exhaustive device check of the fast scale / reciprocal (ztcp_selftest)."""
     assert hip.N.lib().ztcp_selftest() == 0
+
+
+# Payloads of 21, 10 and 31 rows (4k + 1, 4k + 2, 4k + 3) whose sections
+# hold whole 32-group units, so the fused kernels take them: the MAC / verify
+# wave takes rows four at a time and the last total % 4 rows one at a time;
+# 64 pages run the small-batch kernels, 1,100 the row pipelines (5 pages per
+# workgroup, the last one partial).
+PARTIAL_GROUPS = [(1, 8, 64, 64, 1, 2), (1, 2, 256, 0, 1, 0), (1, 8, 128, 64, 1, 2)]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("B", [64, 1100])
+@pytest.mark.parametrize("geo", PARTIAL_GROUPS, ids=lambda g: f"T{g[0]}H{g[1]}D{g[2]}R{g[3]}p{g[4]}r{g[5]}")
+def test_partial_last_mac_group(hip, O, geo, B, dtype):
+    T, Hh, D, R, preset, rm = geo
+    k, v = _pages(61 + B, B, T, Hh, D, R, False, DT[dtype])
+    th = np.arange(B, dtype=np.int64) * 3 + 1
+    exp = O.payload_bytes(preset, rm, T * Hh, D, R, True)
+    assert exp % 64 == 0 and (exp // 64) % 4 != 0
+    got, want = _egress_both(hip, O, k, v, th, preset, rm, R, exp)
+    assert np.array_equal(got, want)
+    err, st, gk, gv, rc, ost, ok, ov = _ingress_both(hip, O, want, th, T, Hh, D, R, False, DT[dtype])
+    assert err is None and rc == 0 and (st == 0).all()
+    assert np.array_equal(gk, ok) and np.array_equal(gv, ov)
