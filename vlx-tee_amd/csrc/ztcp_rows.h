@@ -151,10 +151,16 @@ __device__ __forceinline__ void tm_trace_clear(unsigned long long* timers) {
         __threadfence_block();
     }
 }
+// Trace words are stored through a global pointer: a store through a
+// generic pointer is a flat store, which the wave's LDS waits also wait for,
+// so the traced wave would stall for each trace store's write latency.
+__device__ __forceinline__ void tm_trace_put(uint32_t* trace, int idx, uint32_t v) {
+    if constexpr (kPhaseTimers) ((__attribute__((address_space(1))) uint32_t*)trace)[idx] = v;
+}
 __device__ __forceinline__ void tm_trace(uint32_t* trace, int idx, uint64_t t0) {
     if constexpr (kPhaseTimers) {
         if (trace && idx >= 0 && idx < 4 * kTraceRows && (threadIdx.x & 63) == 0)
-            trace[idx] = (uint32_t)(phase_clock() - t0);
+            tm_trace_put(trace, idx, (uint32_t)(phase_clock() - t0));
     }
 }
 
@@ -405,7 +411,7 @@ __device__ __forceinline__ void mac_rows(const Waiter& wt, const uint32_t* ring,
             tm_add(wt.tm, kTmMacWait + b, waited);
             tm_add(wt.tm, kTmMacMiss + b, 1);
             if (wt.trace && (threadIdx.x & 63) == 0 && r < kTraceRows)
-                wt.trace[2 * kTraceRows + r] = (uint32_t)waited;
+                tm_trace_put(wt.trace, 2 * kTraceRows + r, (uint32_t)waited);
         }
         fl = mac_flags4(ring_flags, ns);
         mac_row_data(ring, pq, ns, b0);
