@@ -14,9 +14,11 @@ the model follows the constants the kernels are built with.
   egress (vlx-tee_amd/csrc/ztcp_egress.hip): producers take code rows in
     order, stage scales per unit, write the ring at the row's payload
     position; a storer wave stores every code row from the ring in payload
-    order and, after a unit's last code row, makes the unit's scale row (its
-    staging slot is then free), publishing that scale rows are stored before
-    it next waits for a row or once four are outstanding; a feeder copies
+    order and, after a unit's last code row, makes the unit's scale row: it
+    keeps it in the unit's staging slot until kScaleGroup rows of the
+    section are made (or the section's last unit is), then stores them and
+    frees their slots, publishing that scale rows are stored before it next
+    waits for a row or once four are outstanding; a feeder copies
     each stored scale row into the ring at its payload position; the MAC
     wave absorbs rows in payload order; a slot is rewritten only once both
     the MAC wave and the storer have passed it.
@@ -49,6 +51,7 @@ def _const(fname, name):
 NBLK = {"i8": 8, "i4": 4, "raw": 16, "e4": 8, "i4g32": 8, "a8": 16}
 LAZY_SCALE_ONLY_AT_END = False  # planted mistake: the storer publishes stored scale rows only when it is done
 IGNORE_STORER = False       # planted mistake: reuse a ring slot once the MAC wave alone has passed it
+GROUP_WITHOUT_SECTION_END = False  # planted mistake: the storer stores held scale rows only in full groups
 FAM0_TASK_SPLIT = False     # planted mistake: ingress splits extension-kind tasks with the reference kinds' divisors
 CONFIGS = {  # sections (kind, units) of the layouts the kernels meet
     "k8v4": [("i8", 16), ("i8", 16), ("i4", 32)],
@@ -188,6 +191,7 @@ def mac_groups(prow, ring, ring_flag, st, KRING):
 
 def egress_model(secs, n_prod, seed):
     KRING, KSTAGE = _const("ztcp_egress.hip", "kRing"), _const("ztcp_egress.hip", "kStage")
+    KGROUP = _const("ztcp_egress.hip", "kScaleGroup")
     prow = payload_rows(secs)
     # code rows in production order, with their payload row and unit
     code, g0 = [], 0
@@ -237,6 +241,7 @@ def egress_model(secs, n_prod, seed):
 
     def storer():
         made, pub = [], 0
+        held = []  # encrypted scale rows kept in their staging slots until their group is complete
         for m in range(len(prow)):
             if prow[m][0] == "code":
                 if pub < len(made) and ring_flag[m % KRING] < m + 1 and not LAZY_SCALE_ONLY_AT_END:
@@ -254,8 +259,16 @@ def egress_model(secs, n_prod, seed):
                     g = code[[c["m"] for c in code].index(m)]["g"]
                     check(staged.get(g, 0) == per_unit[g], "scale row made before its unit was staged")
                     check(stage_units[g % KSTAGE] == g)
-                    stage_flag[g % KSTAGE] = g + 1
-                    made.append(g)
+                    last_of_section = u + 1 == secs[si][1] and not GROUP_WITHOUT_SECTION_END
+                    if len(held) < KGROUP - 1 and not last_of_section:
+                        held.append(g)
+                        yield "ok"
+                        continue
+                    for h in held + [g]:  # stored in order, each slot freed after its stores
+                        check(stage_units[h % KSTAGE] == h, "a held scale row's slot was reused")
+                        stage_flag[h % KSTAGE] = h + 1
+                        made.append(h)
+                    held.clear()
                     yield "ok"
                     if len(made) - pub >= 4 and not LAZY_SCALE_ONLY_AT_END:
                         stored.update(made[pub:]); pub = len(made)
@@ -459,6 +472,21 @@ def test_egress_model_catches_scale_rows_published_only_at_the_end():
         assert not all(egress_model(CONFIGS["k8v4"], 12, seed) for seed in range(5))
     finally:
         LAZY_SCALE_ONLY_AT_END = False
+
+
+def test_egress_model_catches_scale_rows_held_past_their_section():
+    """A planted mistake: a storer that stores held scale rows only in full
+    groups of kScaleGroup keeps a section's last rows (when its unit count is
+    not a multiple of the group) until rows of later sections complete the
+    group, or for good after the last section: the feeder, and through it the
+    MAC wave, wait for rows that are never stored."""
+    global GROUP_WITHOUT_SECTION_END
+    GROUP_WITHOUT_SECTION_END = True
+    try:
+        for cfg in ("tiny", "one_unit_sections"):
+            assert not all(egress_model(CONFIGS[cfg], 12, seed) for seed in range(5)), cfg
+    finally:
+        GROUP_WITHOUT_SECTION_END = False
 
 
 def test_egress_model_catches_a_slot_reused_before_the_storer_read_it():

@@ -21,8 +21,9 @@
 //   * A storer wave (wave 1, SIMD 1) stores every code row from the ring to
 //     the blobs, in payload order, transposed (four lanes per page, 64
 //     contiguous bytes per page per store).  After a unit's last code row
-//     it also makes the unit's scale row: it encrypts the staged scales,
-//     stores them the same way and frees the staging slot.  Producers issue
+//     it also makes the unit's scale row: it encrypts the staged scales in
+//     their slot, and stores them the same way, freeing the slot, together
+//     with the next scale rows of the section, four at a time.  Producers issue
 //     no stores: a wave's wait for its own loads also waits for every store
 //     it issued before them, which exposed the int4 rows' second loads; and
 //     the MAC wave's SIMD is kept free of stores.
@@ -62,7 +63,8 @@ namespace {
 template <int FAM>
 constexpr int egress_waves() { return FAM <= 1 ? 16 : 12; }  // family 2's quantizers need 168 VGPRs
 constexpr int kRing = 28;             // payload rows between their makers and the MAC wave
-constexpr int kStage = 8;             // units whose scales are staged at once
+constexpr int kStage = 9;             // units whose scales are staged at once
+constexpr int kScaleGroup = 4;        // scale rows stored together (at most kScaleGroup - 1 held)
 constexpr int kLdsStage = kRing * kRowWords;
 constexpr int kScaleSlots = 64;       // scale rows the feeder wave may still be waiting for
 constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
@@ -78,6 +80,7 @@ constexpr int kLdsBlobs = kLdsFlags + kNumFlags;      // 64 blob pointers (8-byt
 constexpr int kLdsTimers = kLdsBlobs + 2 * 64;        // phase-timer counters (timer builds only)
 constexpr int kLdsWords = kLdsTimers + kTimerLdsWords;
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
+static_assert(kScaleGroup <= kStage, "held scale rows must leave a staging slot for the unit that completes their group");
 static_assert(kLdsBlobs % 2 == 0 && kLdsTimers % 2 == 0, "blob table and timers must be 8-byte aligned");
 
 __device__ __forceinline__ int32_t total_rows(const Layout& lay) {
@@ -226,9 +229,8 @@ __device__ __forceinline__ uint32_t quant_half_int4g32(const uint32_t (&w)[4][8]
 // the staging slot by then.  Encrypts the staged scales in place, stores the
 // block transposed and frees the staging slot; that the stores have
 // completed is published later (publish_scales).
-__device__ __forceinline__ void scale_row(const ProducerCtx& c, int32_t g, uint32_t block) {
+__device__ __forceinline__ void encrypt_scale_row(const ProducerCtx& c, int32_t g, uint32_t block) {
     const EgressParams& p = *c.p;
-    uint32_t* flags = c.lds + kLdsFlags;
     uint32_t ks[16];
     chacha_block_cached(p.key, c.nc, 1u + block, c.n0, c.n1, c.n2, ks);
     uint32_t* stage = c.lds + kLdsStage + (g % kStage) * kRowWords;
@@ -238,7 +240,12 @@ __device__ __forceinline__ void scale_row(const ProducerCtx& c, int32_t g, uint3
         lds_put_quad(stage, c.lane, q,
                      make_uint4(s.x ^ ks[4 * q], s.y ^ ks[4 * q + 1], s.z ^ ks[4 * q + 2], s.w ^ ks[4 * q + 3]));
     }
-    store_row(stage, c, (uint32_t)kHeader + 64u * block);
+}
+// Stores unit g's encrypted scale row (payload block `block`) from its
+// staging slot and frees the slot.
+__device__ __forceinline__ void store_scale_row(const ProducerCtx& c, int32_t g, uint32_t block) {
+    uint32_t* flags = c.lds + kLdsFlags;
+    store_row(c.lds + kLdsStage + (g % kStage) * kRowWords, c, (uint32_t)kHeader + 64u * block);
     publish(&flags[kFlagStage + g % kStage], (uint32_t)g + 1u);  // the release follows the slot reads
 }
 
@@ -601,6 +608,14 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
 // the storer have both passed it.  Once it has stored a unit's last code row
 // it also makes the unit's scale row (every code row stages its scales before
 // releasing its ring row), so the producers never wait for a unit to fill.
+// A section's scale rows are neighbours in the blob: the storer keeps each
+// encrypted one in its staging slot until it has made the next ones and
+// stores them kScaleGroup at a time (the section's last ones as they come),
+// so that the 128-byte lines they share are written at once instead of one
+// unit apart, when the first half is often evicted and written back alone.
+// No wave waits for a held row before the section's code rows are all
+// stored (the MAC wave reaches the scale rows after them; producers wait
+// for a staging slot only kStage units back).
 // That a scale row's stores have completed is published for the feeder
 // before the storer next waits for a row, or once four are outstanding: the
 // storer issues no loads, so those waits only cover its own stores.  Stores
@@ -627,6 +642,7 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
     __builtin_amdgcn_s_waitcnt(0);
     int32_t r = 0, g0 = 0;      // payload row; quantized units before the section
     int32_t made = 0, pub = 0;  // scale rows made / published as stored
+    int32_t held = 0;           // encrypted scale rows waiting in their slots for the rest of their group
 #pragma unroll
     for (int si = 0; si < 3; ++si) {
         if (si >= p.lay.n_sec) continue;
@@ -649,10 +665,18 @@ __device__ void egress_store_rows(const EgressParams& p, int64_t page0, int ppw,
             publish(&flags[kFlagStored], (uint32_t)r + 1u);  // the release orders the slot reads before it
             if (quant && (cr & (nblk - 1)) == nblk - 1) {
                 const int32_t u = cr / nblk;
-                scale_row(c, g0 + u, sblk + (uint32_t)u);
-                if (++made - pub >= 4) {
-                    publish_scales(flags, pub, made);
-                    pub = made;
+                encrypt_scale_row(c, g0 + u, sblk + (uint32_t)u);
+                if (held < kScaleGroup - 1 && u + 1 < nu) {
+                    ++held;
+                } else {
+#pragma unroll 1
+                    for (int32_t h = u - held; h <= u; ++h) store_scale_row(c, g0 + h, sblk + (uint32_t)h);
+                    made += held + 1;
+                    held = 0;
+                    if (made - pub >= 4) {
+                        publish_scales(flags, pub, made);
+                        pub = made;
+                    }
                 }
             }
         }
