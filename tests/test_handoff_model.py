@@ -303,8 +303,10 @@ def egress_model(secs, n_prod, seed):
 
 def ingress_tasks(secs, L):
     """Decode order of the ingress kernel: per section the scale rows of the
-    first L units, then each unit's code rows followed by the scale row of
-    the unit L further on."""
+    first L units, then the units' code rows two units at a time, with the
+    scale rows of the two units L further on between them (an odd last unit
+    of that part: its code rows, then one scale row), then the code rows of
+    the last L units."""
     tasks, g0, m = [], 0, 0
     for si, (kind, nu) in enumerate(secs):
         nblk = NBLK[kind]
@@ -320,8 +322,10 @@ def ingress_tasks(secs, L):
         else:
             pre, full = min(L, nu), max(nu - L, 0)
             tasks += [scale(u) for u in range(pre)]
-            for u in range(full):
+            for u in range(0, full, 2):
                 tasks += [code(u, j) for j in range(nblk)] + [scale(u + L)]
+                if u + 1 < full:
+                    tasks += [scale(u + 1 + L)] + [code(u + 1, j) for j in range(nblk)]
             for u in range(full, nu):
                 tasks += [code(u, j) for j in range(nblk)]
             g0 += nu
@@ -330,18 +334,19 @@ def ingress_tasks(secs, L):
 
 
 def kernel_task(secs, t, L):
-    """Task t as the ingress kernel computes it (task_info, div_nblk, div_rpu
+    """Task t as the ingress kernel computes it (task_info, div_nblk, div_rpu2
     in ztcp_ingress.hip): integer arithmetic per section, with the divisors
-    chosen by the kind's code rows per unit (family 1: 8 -> /9, 4 -> /5,
-    otherwise /17; family 0 knows only int8 -> /9 and int4 -> /5)."""
+    of a two-unit block chosen by the kind's code rows per unit (family 1:
+    8 -> /18, 4 -> /10, otherwise /34; family 0 knows only int8 -> /18 and
+    int4 -> /10)."""
     fam1 = any(k not in ("i8", "i4", "raw") for k, _ in secs)
     def div_nblk(x, kind):
         return x // NBLK[kind]
-    def div_rpu(x, kind):
+    def div_rpu2(x, kind):
         nblk = NBLK[kind]
         if fam1 and not FAM0_TASK_SPLIT:
-            return x // 9 if nblk == 8 else (x // 5 if nblk == 4 else x // 17)
-        return x // 9 if kind == "i8" else x // 5
+            return x // 18 if nblk == 8 else (x // 10 if nblk == 4 else x // 34)
+        return x // 18 if kind == "i8" else x // 10
     tb = cb = qb = m = 0
     for kind, nu in secs:
         nblk, quant = NBLK[kind], kind != "raw"
@@ -359,10 +364,18 @@ def kernel_task(secs, t, L):
                     scale, u = True, x
                 elif x - pre < full * rpu:
                     x -= pre
-                    u = div_rpu(x, kind)
-                    r = x - u * rpu
-                    scale = r == nblk
-                    u, j = (u + L, 0) if scale else (u, r)
+                    span, pairs = 2 * rpu, full // 2
+                    if x < pairs * span:
+                        p2 = div_rpu2(x, kind)
+                        u0, off = 2 * p2, x - p2 * span
+                    else:
+                        u0, off = full - 1, x - pairs * span
+                    if off < nblk:
+                        u, j = u0, off
+                    elif off <= nblk + 1:
+                        scale, u = True, u0 + L + (off - nblk)
+                    else:
+                        u, j = u0 + 1, off - nblk - 2
                 else:
                     x -= pre + full * rpu
                     u0 = div_nblk(x, kind)

@@ -73,7 +73,7 @@ static_assert(kLdsHeaders % 4 == 0, "header table must be 16-byte aligned");
 static_assert(sizeof(Layout) % 4 == 0, "Layout is copied word by word");
 static_assert(kLdsWords * 4 <= 160 * 1024, "LDS budget of one CU");
 static_assert(kLdsPtrs % 2 == 0, "pointer table must be 8-byte aligned");
-static_assert(kStage >= kLookahead, "a scale row only waits for units whose code rows come before it");
+static_assert(kStage >= kLookahead + 1, "a scale row only waits for units whose code rows come before it");
 
 __device__ __forceinline__ void load_block(const uint8_t* p, uint32_t w[16]) {
 #pragma unroll
@@ -267,9 +267,10 @@ __device__ __forceinline__ void decode_unit(const IngressParams& p, const Layout
 // ---------------------------------------------------------------------------
 
 // Row t of the decode order.  Per section of U units: the scale rows of units
-// 0 .. L-1, then for each unit u its code rows followed by the scale row of
-// unit u + L (L = kLookahead), so a unit's scales are decrypted while the
-// units before it are being decoded.
+// 0 .. L-1, then the units' code rows, two units at a time with the scale
+// rows of units u + L and u + 1 + L (L = kLookahead) between them (task_info
+// below), so a unit's scales are decrypted while the units before it are
+// being decoded.
 struct Task {
     int32_t valid;
     int32_t scale;    // 1: scale row of unit u
@@ -290,14 +291,20 @@ __device__ __forceinline__ int32_t div_nblk(int32_t x, int32_t kind) {  // nblk 
     return kind == kSecInt8 ? x / 8 : (kind == kSecInt4 ? x / 4 : x / 16);
 }
 template <int FAM>
-__device__ __forceinline__ int32_t div_rpu(int32_t x, int32_t kind) {  // nblk + 1 = 9, 5, 17
+__device__ __forceinline__ int32_t div_rpu2(int32_t x, int32_t kind) {  // 2 (nblk + 1) = 18, 10, 34
     if constexpr (FAM == 1) {
         const int32_t nblk = code_rows_per_unit(kind);
-        return nblk == 8 ? x / 9 : (nblk == 4 ? x / 5 : x / 17);
+        return nblk == 8 ? x / 18 : (nblk == 4 ? x / 10 : x / 34);
     }
-    return kind == kSecInt8 ? x / 9 : x / 5;
+    return kind == kSecInt8 ? x / 18 : x / 10;
 }
 
+// Task t of the workgroup layout.  A quantized section hands out the scale
+// rows of its first kLookahead units, then its units' code rows two units
+// at a time with the scale rows of the two units kLookahead further on
+// between them: code rows of u, scale rows of u + L and u + 1 + L, code
+// rows of u + 1.  Neighbouring scale rows share 128-byte lines in the blob,
+// and decoders that take them one after the other read those lines at once.
 template <int FAM>
 __device__ __forceinline__ Task task_info(const Layout& lay, int32_t t) {
     Task k{};
@@ -321,10 +328,26 @@ __device__ __forceinline__ Task task_info(const Layout& lay, int32_t t) {
                     k.scale = 1;
                     k.u = x;
                 } else if ((x -= pre) < full * s.rpu) {
-                    const int32_t u = div_rpu<FAM>(x, s.kind), r = x - u * s.rpu;
-                    k.scale = r == s.nblk;
-                    k.u = k.scale ? u + kLookahead : u;
-                    k.j = k.scale ? 0 : r;
+                    const int32_t span = 2 * s.rpu, pairs = full >> 1;
+                    int32_t u0, off;
+                    if (x < pairs * span) {
+                        const int32_t p2 = div_rpu2<FAM>(x, s.kind);
+                        u0 = 2 * p2;
+                        off = x - p2 * span;
+                    } else {  // an odd last unit: its code rows, then one scale row
+                        u0 = full - 1;
+                        off = x - pairs * span;
+                    }
+                    if (off < s.nblk) {
+                        k.u = u0;
+                        k.j = off;
+                    } else if (off <= s.nblk + 1) {
+                        k.scale = 1;
+                        k.u = u0 + kLookahead + (off - s.nblk);
+                    } else {
+                        k.u = u0 + 1;
+                        k.j = off - s.nblk - 2;
+                    }
                 } else {
                     x -= full * s.rpu;
                     const int32_t u = div_nblk<FAM>(x, s.kind);
