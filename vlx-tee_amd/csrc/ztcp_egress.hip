@@ -23,7 +23,7 @@
 //     contiguous bytes per page per store).  After a unit's last code row
 //     it also makes the unit's scale row: it encrypts the staged scales in
 //     their slot, and stores them the same way, freeing the slot, together
-//     with the next scale rows of the section, four at a time.  Producers issue
+//     with the next scale rows of the section, eight at a time.  Producers issue
 //     no stores: a wave's wait for its own loads also waits for every store
 //     it issued before them, which exposed the int4 rows' second loads; and
 //     the MAC wave's SIMD is kept free of stores.
@@ -62,9 +62,9 @@ namespace {
 // memory.
 template <int FAM>
 constexpr int egress_waves() { return FAM <= 1 ? 16 : 12; }  // family 2's quantizers need 168 VGPRs
-constexpr int kRing = 28;             // payload rows between their makers and the MAC wave
-constexpr int kStage = 9;             // units whose scales are staged at once
-constexpr int kScaleGroup = 4;        // scale rows stored together (at most kScaleGroup - 1 held)
+constexpr int kRing = 24;             // payload rows between their makers and the MAC wave
+constexpr int kStage = 13;            // units whose scales are staged at once
+constexpr int kScaleGroup = 8;        // scale rows stored together (at most kScaleGroup - 1 held)
 constexpr int kLdsStage = kRing * kRowWords;
 constexpr int kScaleSlots = 64;       // scale rows the feeder wave may still be waiting for
 constexpr int kLdsFlags = kLdsStage + kStage * kRowWords;
