@@ -613,9 +613,10 @@ __device__ void egress_scale_feed(const EgressParams& p, uint32_t* lds) {
 // stores them kScaleGroup at a time (the section's last ones as they come),
 // so that the 128-byte lines they share are written at once instead of one
 // unit apart, when the first half is often evicted and written back alone.
-// No wave waits for a held row before the section's code rows are all
-// stored (the MAC wave reaches the scale rows after them; producers wait
-// for a staging slot only kStage units back).
+// Holding them creates no cycle of waits: the MAC wave reaches a section's
+// scale rows after all of its code rows, and a producer of unit g waits for
+// the slot of unit g - kStage, which is stored at the latest with unit
+// g - kStage + kScaleGroup - 1, a unit before g (kScaleGroup <= kStage).
 // That a scale row's stores have completed is published for the feeder
 // before the storer next waits for a row, or once four are outstanding: the
 // storer issues no loads, so those waits only cover its own stores.  Stores
